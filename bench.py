@@ -1,0 +1,224 @@
+#!/usr/bin/env python3
+"""Benchmark of the GGUF quantized linear path on one MI355X (BASELINE.json's metric).
+
+Workload (the configuration the metric is quoted on): the Q4_K and Q6_K
+decode GEMV at the 27B-class dense shapes (N, K) in {(7168, 5120) qkv, (5120, 5120) o_proj,
+(34816, 5120) gate_up, (5120, 17408) down}, batch rows M = 8 (default), bf16 activations.
+One step = one grouped launch per (type, shape) shard over one batch, i.e. every shard's
+packed weights streamed once.  Weights are random valid GGUF blocks generated on the GPU
+(kernel time does not depend on the values) in `--copies` rotating copies (> 1 GB in total) so
+the 256 MB Infinity Cache cannot serve a repeat; launches are captured in HIP graphs and timed
+with events on the launch stream.
+
+value = packed GGUF bytes per step / time per step (GB/s; inputs resident in HBM).
+roofline = the dominant kernel (the shard with the largest launch time): packed bytes per
+launch / its average launch duration vs 8 TB/s.  The M = 2048 dequant-GEMM (config 4, Q4_K
+gate_up) is reported beside it as TFLOP/s vs 2.5 PFLOP/s bf16.
+cpu_baseline = the reference CPU path (gguf-py's dequantizer, as restated by oracle/, plus
+torch.matmul in fp32) on a bounded row sample of the Q4_K / Q6_K gate_up shards.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for _p in (REPO, os.path.join(REPO, "hyperqwen-rtx4080s32_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0        # MI355X dense bf16 MFMA
+Q4_K, Q6_K = 12, 14
+SHAPES = [("qkv", 7168, 5120), ("o_proj", 5120, 5120), ("gate_up", 34816, 5120), ("down", 5120, 17408)]
+METRIC = "packed-weight GB/s (% HBM peak) at M=1-32; bf16 TFLOP/s (% MFMA) at M=2048"
+
+
+def _time_graph(graph, reps, torch):
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        graph.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def _capture(fn, torch):
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fn()                                  # warm the allocator outside the capture
+    torch.cuda.current_stream().wait_stream(st)
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    """The reference CPU path on a bounded sample: oracle dequant (numpy, one thread) + fp32
+    torch.matmul (torch's threads) of row samples of the Q4_K and Q6_K gate_up shards, M = 8."""
+    import numpy as np
+    import torch
+
+    from oracle import ggml_ref as G
+
+    rng = np.random.default_rng(0)
+    K, M = 5120, 8
+    x = torch.randn(M, K)
+
+    def one(rows):
+        t_deq = t_mm = 0.0
+        nbytes = 0
+        for wt in (Q4_K, Q6_K):
+            raw = G.random_blocks(rng, rows, K, wt)
+            t0 = time.perf_counter()
+            w = torch.from_numpy(G.dequantize(raw, wt))
+            t1 = time.perf_counter()
+            y = x @ w.T
+            t2 = time.perf_counter()
+            assert y.shape == (M, rows)
+            t_deq += t1 - t0
+            t_mm += t2 - t1
+            nbytes += raw.nbytes
+        return t_deq, t_mm, nbytes
+
+    d, m, b = one(256)                                       # calibrate
+    rows = int(max(256, min(34816, 256 * (seconds / 3) / max(d + m, 1e-3))))
+    runs = [one(rows) for _ in range(3)]
+    td = statistics.median(r[0] for r in runs)
+    tm = statistics.median(r[1] for r in runs)
+    nbytes = runs[0][2]
+    return {"value": round(nbytes / (td + tm) / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"Q4_K+Q6_K gate_up rows 0..{rows} of 34816 x K=5120, M={M}: oracle dequant "
+                      f"{td * 1e3:.1f} ms (1 thread) + torch fp32 matmul {tm * 1e3:.1f} ms, median of 3",
+            "dequant_ms": round(td * 1e3, 2), "matmul_ms": round(tm * 1e3, 2)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--m", type=int, default=8, help="batch rows of the decode GEMV (1..32)")
+    ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 1 GB in total)")
+    ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--detail", action="store_true", help="print the per-shard table to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the GGUF linear path has no collective; "
+              "sharding is design-only). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import gguf_hip
+    from gguf_hip.synth import random_shard
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M = args.m
+    shards = []                     # (type, name, N, K, [GroupedLayer per copy], bytes)
+    for wt in (Q4_K, Q6_K):
+        for name, N, K in SHAPES:
+            gls = []
+            for c in range(args.copies):
+                W = random_shard(N, K, wt, dev, seed=1000 * c + N + wt)
+                gls.append(gguf_hip.pack_layer([W], [N], [wt]))
+                nbytes = W.numel()
+                del W
+            shards.append((wt, name, N, K, gls, nbytes))
+    torch.cuda.empty_cache()
+    xs = {K: torch.randn(M, K, device=dev).to(torch.bfloat16) for K in {s[3] for s in shards}}
+    step_bytes = sum(s[5] for s in shards)
+
+    # one graph per copy: every shard once (one step)
+    def step_fn(c):
+        def f():
+            for wt, name, N, K, gls, nb in shards:
+                gguf_hip.mul_mat_grouped(xs[K], gls[c])
+        return f
+
+    graphs = [_capture(step_fn(c), torch) for c in range(args.copies)]
+    for i in range(args.warmup):
+        graphs[i % args.copies].replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    s.record()
+    for i in range(args.steps):
+        graphs[i % args.copies].replay()
+    e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = s.elapsed_time(e) / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # per-shard launch time (graph of every copy once; average per launch)
+    rows = []
+    for wt, name, N, K, gls, nb in shards:
+        def f(gls=gls, K=K):
+            for gl in gls:
+                gguf_hip.mul_mat_grouped(xs[K], gl)
+        g = _capture(f, torch)
+        g.replay()
+        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / len(gls)
+        plan = gls[0].plans[[4, 8, 16, 32].index(next(b for b in (4, 8, 16, 32) if M <= b)) * 10:][:10]
+        rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
+                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "split": plan[4], "wgs": plan[5]})
+        del g
+    dom = max(rows, key=lambda r: r["us"])
+    dom_bytes = next(s[5] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
+    achieved = dom_bytes / (dom["us"] * 1e-6) / 1e9
+    if args.detail:
+        for r in rows:
+            print(json.dumps(r), file=sys.stderr)
+
+    gemm = None
+    if args.gemm_m:
+        del graphs
+        Mg = args.gemm_m
+        wt, name, N, K, gls, nb = next(s for s in shards if s[0] == Q4_K and s[1] == "gate_up")
+        xg = torch.randn(Mg, K, device=dev).to(torch.bfloat16)
+
+        def fg():
+            for gl in gls:
+                gguf_hip.mul_mat_grouped(xg, gl)
+        g = _capture(fg, torch)
+        g.replay()
+        t = statistics.median(_time_graph(g, 3, torch) for _ in range(3)) / len(gls)
+        tflops = 2.0 * Mg * N * K / (t * 1e-3) / 1e12
+        gemm = {"type": "Q4_K", "shard": "gate_up", "N": N, "K": K, "M": Mg, "ms": round(t, 4),
+                "TFLOPs": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic: random valid GGUF blocks generated on the GPU",
+        "config": {"workload": f"BASELINE config 2: Q4_K + Q6_K decode GEMV, M={M}, shapes "
+                               "qkv 7168x5120, o_proj 5120x5120, gate_up 34816x5120, down 5120x17408",
+                   "M": M, "copies": args.copies, "bytes_per_step": step_bytes,
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4), "wall_s": round(wall, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"{dom['type']} {dom['shard']} {dom['N']}x{dom['K']} M={M}",
+                     "launch_us": dom["us"], "bytes_per_launch": dom_bytes},
+        "shards": rows,
+        "gemm": gemm,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

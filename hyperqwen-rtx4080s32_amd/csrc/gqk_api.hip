@@ -1,0 +1,236 @@
+// gqk_api.hip - the C ABI (include/gguf_hip.h): argument checks, the launch plans, errors.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <algorithm>
+#include <string>
+#include <vector>
+#include "gguf_hip.h"
+#include "gqk_common.h"
+#include "gqk_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(GQK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return GQK_OK;
+}
+
+// GEMV workgroup target when the caller gives none: about four 4-wave workgroups per CU of a
+// 256-CU MI355X, so every SIMD holds four waves streaming weights.
+constexpr int kDefaultTargetWgs = 1024;
+
+}  // namespace
+
+extern "C" {
+
+const char* gqk_last_error(void) { return g_err.c_str(); }
+
+int gqk_version(void) { return 100; }
+
+int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes) {
+  const gqk_type* t = gqk_type_get(ggml_type);
+  if (!t) return fail(GQK_ERR_TYPE, "unsupported GGML type %d", ggml_type);
+  if (!info) return fail(GQK_ERR_ARG, "gqk_type_info: info is NULL");
+  info[0] = t->block_weights;
+  info[1] = t->block_bytes;
+  info[2] = t->rec;
+  info[3] = t->nplanes;
+  if (planes)
+    for (int p = 0; p < t->nplanes; ++p) {
+      planes[5 * p + 0] = t->planes[p].size;
+      planes[5 * p + 1] = t->planes[p].nseg;
+      planes[5 * p + 2] = t->planes[p].seg_off;
+      planes[5 * p + 3] = t->planes[p].seg_len;
+      planes[5 * p + 4] = t->planes[p].seg_stride;
+    }
+  return GQK_OK;
+}
+
+int gqk_dequantize(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, int64_t K, void* out,
+                   int64_t ld_out, int out_dtype, void* stream) {
+  const gqk_type* t = gqk_type_get(ggml_type);
+  if (!t) return fail(GQK_ERR_TYPE, "unsupported GGML type %d", ggml_type);
+  if (n < 0 || K < 0 || K % t->block_weights != 0)
+    return fail(GQK_ERR_SHAPE, "dequantize: K=%lld is not a multiple of the type's %d-weight block", (long long)K,
+                t->block_weights);
+  if (out_dtype < 0 || out_dtype > 2) return fail(GQK_ERR_ARG, "dequantize: out_dtype %d", out_dtype);
+  if (n == 0 || K == 0) return GQK_OK;
+  if (!W || !out) return fail(GQK_ERR_ARG, "dequantize: null pointer");
+  if (w_row_stride < K / t->block_weights * t->block_bytes)
+    return fail(GQK_ERR_SHAPE, "dequantize: row stride %lld < row bytes %lld", (long long)w_row_stride,
+                (long long)(K / t->block_weights * t->block_bytes));
+  if (ld_out < K) return fail(GQK_ERR_SHAPE, "dequantize: ld_out %lld < K %lld", (long long)ld_out, (long long)K);
+  int rc = gqk::launch_dequant(ggml_type, W, w_row_stride, n, K, out, ld_out, out_dtype, (hipStream_t)stream);
+  if (rc) return fail(rc, "dequantize: type %d", ggml_type);
+  return check_launch("dequantize");
+}
+
+int64_t gqk_tiles_bytes(int ggml_type, int64_t n, int64_t K) {
+  const gqk_type* t = gqk_type_get(ggml_type);
+  if (!t) return fail(GQK_ERR_TYPE, "unsupported GGML type %d", ggml_type);
+  if (n < 0 || K < 0 || K % 256 != 0)
+    return fail(GQK_ERR_SHAPE, "tiles: K=%lld is not a multiple of 256", (long long)K);
+  return (n + 63) / 64 * 64 * (K / 256) * t->rec;
+}
+
+static int repack_common(const void* W, int64_t stride, int type, int64_t n, int64_t K, void* tiles, bool to_tiles,
+                         void* stream) {
+  const gqk_type* t = gqk_type_get(type);
+  if (!t) return fail(GQK_ERR_TYPE, "unsupported GGML type %d", type);
+  if (n < 0 || K < 0 || K % 256 != 0) return fail(GQK_ERR_SHAPE, "repack: K=%lld is not a multiple of 256", (long long)K);
+  if (n == 0 || K == 0) return GQK_OK;
+  if (!W || !tiles) return fail(GQK_ERR_ARG, "repack: null pointer");
+  if (stride < K / 256 * t->rec)
+    return fail(GQK_ERR_SHAPE, "repack: row stride %lld < row bytes %lld", (long long)stride, (long long)(K / 256 * t->rec));
+  int rc = gqk::launch_repack(type, W, stride, n, K, tiles, to_tiles, (hipStream_t)stream);
+  if (rc) return fail(rc, "repack: type %d", type);
+  return check_launch(to_tiles ? "repack" : "unrepack");
+}
+
+int gqk_repack(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, int64_t K, void* tiles, void* stream) {
+  return repack_common(W, w_row_stride, ggml_type, n, K, tiles, true, stream);
+}
+
+int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W, int64_t w_row_stride, void* stream) {
+  return repack_common(W, w_row_stride, ggml_type, n, K, (void*)tiles, false, stream);
+}
+
+int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
+             int64_t desc_capacity, gqk_plan_info* info) {
+  if (!shards || nshards <= 0 || !info) return fail(GQK_ERR_ARG, "plan: no shards / info");
+  if (K <= 0 || K % 256 != 0) return fail(GQK_ERR_SHAPE, "plan: K=%lld is not a positive multiple of 256", (long long)K);
+  if (M <= 0) return fail(GQK_ERR_SHAPE, "plan: M=%d", M);
+  const int64_t nb = K / 256;
+  if (nb > (1 << 30)) return fail(GQK_ERR_SHAPE, "plan: K too large");
+  int64_t n_total = 0, expect_off = 0;
+  int first_type = shards[0].ggml_type;
+  bool mixed = false;
+  for (int i = 0; i < nshards; ++i) {
+    const gqk_type* t = gqk_type_get(shards[i].ggml_type);
+    if (!t) return fail(GQK_ERR_TYPE, "plan: shard %d has unsupported GGML type %d", i, shards[i].ggml_type);
+    if (shards[i].n <= 0) return fail(GQK_ERR_SHAPE, "plan: shard %d has %lld rows", i, (long long)shards[i].n);
+    if (shards[i].offset != expect_off)
+      return fail(GQK_ERR_SHAPE, "plan: shard %d at byte %lld, expected %lld (shards are packed back to back)", i,
+                  (long long)shards[i].offset, (long long)expect_off);
+    if (shards[i].offset % 16 != 0) return fail(GQK_ERR_SHAPE, "plan: shard %d offset not 16-byte aligned", i);
+    expect_off += (shards[i].n + 63) / 64 * 64 * nb * t->rec;
+    n_total += shards[i].n;
+    mixed |= shards[i].ggml_type != first_type;
+  }
+  if (n_total >= (int64_t)1 << 31) return fail(GQK_ERR_SHAPE, "plan: %lld output columns", (long long)n_total);
+
+  gqk_plan_info pi{};
+  pi.types_mask = mixed ? 0 : first_type;
+  pi.nb = (int32_t)nb;
+  pi.n_total = n_total;
+  std::vector<int32_t> rows;
+  auto row = [&](int i, int64_t tile0, int ntiles, int64_t kb0, int64_t kb1, int split, int64_t col0) {
+    int32_t r[GQK_DESC_WORDS] = {0};
+    r[D_TYPE] = shards[i].ggml_type;
+    r[D_OFF_LO] = (int32_t)(uint32_t)(shards[i].offset & 0xFFFFFFFF);
+    r[D_OFF_HI] = (int32_t)(shards[i].offset >> 32);
+    r[D_TILE0] = (int32_t)tile0;
+    r[D_NTILES] = ntiles;
+    r[D_KB0] = (int32_t)kb0;
+    r[D_KB1] = (int32_t)kb1;
+    r[D_SPLIT] = split;
+    r[D_COL0] = (int32_t)(col0 + tile0 * 64);
+    r[D_NVALID] = (int32_t)std::min<int64_t>((int64_t)ntiles * 64, shards[i].n - tile0 * 64);
+    r[D_NB] = (int32_t)nb;
+    rows.insert(rows.end(), r, r + GQK_DESC_WORDS);
+  };
+  if (M <= 32) {
+    pi.form = GQK_FORM_GEMV;
+    pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
+    pi.m_max = 4 * pi.g;
+    int64_t w0 = 0;
+    for (int i = 0; i < nshards; ++i) w0 += ((shards[i].n + 63) / 64 + 3) / 4;
+    const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWgs;
+    int64_t split = (target + w0 - 1) / w0;
+    split = std::max<int64_t>(1, std::min<int64_t>(split, std::max<int64_t>(1, nb / 2)));
+    pi.split = (int32_t)split;
+    int64_t col0 = 0;
+    for (int i = 0; i < nshards; ++i) {
+      int64_t ntile = (shards[i].n + 63) / 64;
+      for (int64_t t0 = 0; t0 < ntile; t0 += 4)
+        for (int64_t s = 0; s < split; ++s)   // balanced partition: every split owns >= 1 super-block
+          row(i, t0, (int)std::min<int64_t>(4, ntile - t0), s * nb / split, (s + 1) * nb / split, (int)s, col0);
+      col0 += shards[i].n;
+    }
+    pi.workspace_bytes = split > 1 ? (int64_t)split * pi.m_max * n_total * 4 : 0;
+  } else {
+    pi.form = GQK_FORM_GEMM;
+    pi.bm = M <= 64 ? 64 : 128;
+    pi.m_max = 1 << 30;
+    pi.split = 1;
+    int64_t col0 = 0;
+    for (int i = 0; i < nshards; ++i) {
+      int64_t ntile = (shards[i].n + 63) / 64;
+      for (int64_t t0 = 0; t0 < ntile; t0 += 2) row(i, t0, (int)std::min<int64_t>(2, ntile - t0), 0, nb, 0, col0);
+      col0 += shards[i].n;
+    }
+    pi.workspace_bytes = 0;
+  }
+  pi.n_desc = (int32_t)(rows.size() / GQK_DESC_WORDS);
+  *info = pi;
+  if (desc) {
+    if (desc_capacity < (int64_t)rows.size())
+      return fail(GQK_ERR_ARG, "plan: descriptor capacity %lld < %lld words", (long long)desc_capacity,
+                  (long long)rows.size());
+    memcpy(desc, rows.data(), rows.size() * sizeof(int32_t));
+  }
+  return GQK_OK;
+}
+
+int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
+               int M, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!info) return fail(GQK_ERR_ARG, "linear: info is NULL");
+  if (M < 0) return fail(GQK_ERR_SHAPE, "linear: M=%d", M);
+  if (M == 0) return GQK_OK;
+  if (!packed || !desc_dev || !x || !y) return fail(GQK_ERR_ARG, "linear: null pointer");
+  const int64_t K = (int64_t)info->nb * 256;
+  if (ldx < K || ldy < info->n_total)
+    return fail(GQK_ERR_SHAPE, "linear: ldx %lld < K %lld or ldy %lld < columns %lld", (long long)ldx, (long long)K,
+                (long long)ldy, (long long)info->n_total);
+  if (((uintptr_t)x & 15) || (ldx & 7))
+    return fail(GQK_ERR_SHAPE, "linear: x must be 16-byte aligned with a row stride that is a multiple of 8");
+  if (info->form == GQK_FORM_GEMV) {
+    if (M > info->m_max) return fail(GQK_ERR_FORM, "linear: M=%d above the GEMV plan's %d rows", M, info->m_max);
+    if (info->g != 1 && info->g != 2 && info->g != 4 && info->g != 8) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
+    if (info->split > 1) {
+      int64_t need = (int64_t)info->split * M * info->n_total * 4;
+      if (!workspace || workspace_bytes < need)
+        return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);
+    }
+    int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, y,
+                              ldy, (float*)workspace, info->split, info->n_total, (hipStream_t)stream);
+    if (rc) return fail(rc, "linear: GEMV launch form");
+    return check_launch("linear (GEMV)");
+  }
+  if (info->form == GQK_FORM_GEMM) {
+    if (M <= 32) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
+    if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
+    int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
+                              info->bm, (hipStream_t)stream);
+    if (rc) return fail(rc, "linear: GEMM launch form bm=%d", info->bm);
+    return check_launch("linear (GEMM)");
+  }
+  return fail(GQK_ERR_FORM, "linear: unknown form %d", info->form);
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+/* gguf_hip.h - C ABI of the MI355X (gfx950) GGUF quantized linear path.
+ *
+ * A drop-in for the out-of-tree vLLM GGUF plugin's linear path: the entry points below are
+ * what that plugin's Python binds for (a) dequantize(W, type, shape), (b) the load-time tile
+ * repack and grouped-layer preparation, and (c) the grouped matmul op called from
+ * GGUFLinearMethod.apply(layer, x, bias).  Plain C: raw device pointers, sizes and a HIP stream
+ * passed as void*.  No allocation happens inside any entry point: outputs, tiles and workspace
+ * are owned by the caller (torch), and every launch goes on the caller's stream.
+ *
+ * Status: every int-returning function returns GQK_OK (0) or a negative GQK_ERR_* code;
+ * gqk_last_error() returns a thread-local message for the last failure on the calling thread.
+ */
+#ifndef GGUF_HIP_H
+#define GGUF_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GQK_OK 0
+#define GQK_ERR_TYPE (-1)  /* GGML type without a kernel (reference: NotImplementedError,
+                              gguf-plugin/gluon/interface.py:78-79) */
+#define GQK_ERR_SHAPE (-2) /* shape / size / alignment contract broken (reference: AssertionError,
+                              gguf-plugin/gluon/tiles_grouped.py:1211-1263) */
+#define GQK_ERR_FORM (-3)  /* plan does not serve this launch (M outside the plan's range) */
+#define GQK_ERR_HIP (-4)   /* HIP runtime error at launch */
+#define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
+
+#define GQK_FORM_GEMV 1 /* M <= 32: in-register decode GEMV (MFMA 4x4x4 per scale group) */
+#define GQK_FORM_GEMM 2 /* M > 32: LDS-dequant bf16 MFMA GEMM */
+
+#define GQK_DTYPE_F32 0
+#define GQK_DTYPE_BF16 1
+#define GQK_DTYPE_F16 2
+
+/* One shard of a grouped layer: its rows sit at byte `offset` of the packed tile buffer. */
+typedef struct gqk_shard {
+  int32_t ggml_type;
+  int32_t reserved;
+  int64_t n;      /* output rows */
+  int64_t offset; /* byte offset of the shard's tiles in the packed buffer */
+} gqk_shard;
+
+/* Launch plan of a grouped layer for one batch-row bucket (filled by gqk_plan). */
+typedef struct gqk_plan_info {
+  int32_t form;       /* GQK_FORM_GEMV or GQK_FORM_GEMM */
+  int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
+  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4, 8) */
+  int32_t bm;         /* GEMM: tokens per workgroup (64, 128) */
+  int32_t split;      /* GEMV: split-K factor (partials + fixed-order reduce when > 1) */
+  int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
+  int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
+  int32_t nb;         /* K / 256 */
+  int64_t n_total;    /* output columns: sum of the shards' rows */
+  int64_t workspace_bytes; /* device workspace gqk_linear needs at M = m_max */
+} gqk_plan_info;
+
+/* Last error message of the calling thread ("" when none). */
+const char* gqk_last_error(void);
+
+/* Library version: major * 10000 + minor * 100 + patch. */
+int gqk_version(void);
+
+/* Host-only metadata of a GGML type: info[0..3] = weights per block, bytes per block, bytes per
+ * 256 weights, number of tile planes; planes (if not NULL, 5 ints per plane) = bytes per row,
+ * segments, first raw offset, segment bytes, segment stride.  Replaces the reference's tile
+ * registry TILE_TYPES (gguf-plugin/gluon/tiles.py:24-36) and gguf.GGML_QUANT_SIZES. */
+int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes);
+
+/* Dequantize n rows of K weights of `ggml_type` (raw GGUF blocks, row stride in bytes) into
+ * out[n, ld_out] of out_dtype (GQK_DTYPE_*): fp32 bit-exact with gguf-py's dequantizer, bf16 /
+ * fp16 the round-to-nearest-even of it.  Replaces ops.ggml_dequantize(W, type, m, n, dtype)
+ * (gguf-plugin/patches/gguf-prefill-dispatch.patch:42-45, gguf-plugin/gluon/tiles.py:147-149). */
+int gqk_dequantize(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, int64_t K, void* out,
+                   int64_t ld_out, int out_dtype, void* stream);
+
+/* Bytes of the tile layout of an n x K shard (< 0: error code).  K % 256 == 0. */
+int64_t gqk_tiles_bytes(int ggml_type, int64_t n, int64_t K);
+
+/* Raw GGUF rows -> CDNA4 plane-major tiles (64-row tiles x 256-weight super-blocks, rows past n
+ * zero).  Replaces repack_tiles (gguf-plugin/gluon/tiles.py:128-130). */
+int gqk_repack(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, int64_t K, void* tiles, void* stream);
+
+/* Tiles -> raw GGUF rows (bit-exact inverse of gqk_repack).  Replaces unrepack_tiles
+ * (gguf-plugin/gluon/tiles.py:56-67). */
+int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W, int64_t w_row_stride, void* stream);
+
+/* Host-only: the launch plan of a grouped layer (shards packed back to back, all of K columns)
+ * for batch rows M: fills *info and, if desc is not NULL and desc_capacity (int32 words) is
+ * enough, the descriptor table (16 int32 per row) to upload to the device.  target_wgs > 0
+ * overrides the GEMV split heuristic's workgroup target (0 = default).  Replaces
+ * prepare_grouped_layer / descriptors / grouped_split_for
+ * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
+int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
+             int64_t desc_capacity, gqk_plan_info* info);
+
+/* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T over the grouped layer's shards (columns in shard
+ * order), on `stream`.  desc_dev: the plan's descriptor table in device memory; workspace: at
+ * least info->workspace_bytes of device memory when info->split > 1 (else may be NULL).  M must
+ * be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
+ * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
+ * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
+int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
+               int M, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GGUF_HIP_H */

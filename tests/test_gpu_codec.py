@@ -1,0 +1,103 @@
+"""GPU parity of the dequantizer and the tile repack (through the C ABI), bit-exact against the
+oracle: fp32 equal bits, bf16 / fp16 the round-to-nearest-even of the oracle's fp32."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ggml_ref as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_dequantize_bit_exact(dev, wt):
+    import gguf_hip
+
+    rng = np.random.default_rng(100 + wt)
+    n, K = 70, 768
+    raw = G.random_blocks(rng, n, K, wt)
+    ref = G.dequantize(raw, wt)
+    W = _to_dev(raw, dev)
+    got = gguf_hip.dequantize(W, wt, (n, K), torch.float32).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    ref_t = torch.from_numpy(ref)
+    for dt in (torch.bfloat16, torch.float16):
+        g = gguf_hip.dequantize(W, wt, (n, K), dt).cpu()
+        assert torch.equal(g.view(torch.int16), ref_t.to(dt).view(torch.int16)), dt
+    # the plugin's spelling (m rows, n columns, fp16 default)
+    g16 = gguf_hip.ggml_dequantize(W, wt, n, K)
+    assert g16.dtype == torch.float16 and torch.equal(g16.cpu(), ref_t.to(torch.float16))
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_dequantize_strided_rows_and_quantized_weights(dev, wt):
+    import gguf_hip
+
+    rng = np.random.default_rng(200 + wt)
+    n, K = 33, 512
+    raw = G.make_weights(rng, n, K, wt)
+    rb = raw.shape[1]
+    big = np.zeros((n, rb + 40), np.uint8)
+    big[:, 7:7 + rb] = raw                                   # a shard view inside wider rows
+    Wv = _to_dev(big, dev)[:, 7:7 + rb]
+    assert Wv.stride(0) == rb + 40
+    got = gguf_hip.dequantize(Wv, wt, (n, K)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), G.dequantize(raw, wt).view(np.uint32))
+
+
+@pytest.mark.parametrize("wt", [G.Q4_0, G.Q5_0, G.Q8_0, G.IQ4_NL], ids=lambda t: G.NAMES[t])
+def test_dequantize_32_block_types_any_k(dev, wt):
+    import gguf_hip
+
+    rng = np.random.default_rng(300 + wt)
+    raw = G.random_blocks(rng, 5, 96, wt)
+    got = gguf_hip.dequantize(_to_dev(raw, dev), wt, (5, 96)).cpu().numpy()
+    assert np.array_equal(got, G.dequantize(raw, wt))
+
+
+def _np_repack(raw, wt, n, K, planes, rec):
+    nb = K // 256
+    ntiles = -(-n // 64)
+    rows = np.zeros((ntiles * 64, nb, rec), np.uint8)
+    rows[:n] = raw.reshape(n, nb, rec)
+    out = np.zeros((ntiles, nb, 64 * rec), np.uint8)
+    poff = 0
+    for size, nseg, off, seglen, stride in planes:
+        idx = np.concatenate([np.arange(off + s * stride, off + s * stride + seglen) for s in range(nseg)])
+        block = rows[:, :, idx].reshape(ntiles, 64, nb, size).transpose(0, 2, 1, 3).reshape(ntiles, nb, 64 * size)
+        out[:, :, 64 * poff:64 * (poff + size)] = block
+        poff += size
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_repack_layout_and_roundtrip(dev, wt):
+    import gguf_hip
+
+    rng = np.random.default_rng(400 + wt)
+    n, K = 70, 768
+    raw = G.random_blocks(rng, n, K, wt)
+    W = _to_dev(raw, dev)
+    tiles = gguf_hip.repack_tiles(W, n, wt)
+    _, _, rec, _ = gguf_hip.type_info(wt)
+    expect = _np_repack(raw, wt, n, K, gguf_hip.type_planes(wt), rec)
+    assert tiles.numel() == expect.size == gguf_hip.tiles_bytes(wt, n, K)
+    assert np.array_equal(tiles.cpu().numpy(), expect)
+    back = gguf_hip.unrepack_tiles(tiles, n, K, wt)
+    assert torch.equal(back.cpu(), torch.from_numpy(raw))
+    w = gguf_hip.dequantize_tiles(tiles, n, K, wt, torch.float32).cpu().numpy()
+    assert np.array_equal(w, G.dequantize(raw, wt))
+
+
+def test_repack_rejects_bad_k(dev):
+    import gguf_hip
+
+    W = torch.zeros((4, 18 * 3), dtype=torch.uint8, device=dev)
+    with pytest.raises(ValueError):
+        gguf_hip.repack_tiles(W, 4, G.Q4_0)                  # 96 weights: not whole super-blocks
+    with pytest.raises(NotImplementedError):
+        gguf_hip.dequantize(torch.zeros((4, 66), dtype=torch.uint8, device=dev), 16, (4, 256))

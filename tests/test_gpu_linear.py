@@ -1,0 +1,180 @@
+"""GPU parity of the grouped linear op (GEMV form M <= 32, GEMM form M > 32) against the
+oracle: y = x @ dequant(W)^T in fp64 on the oracle's weights, tolerance 1e-2 relative to each
+output row's max |y| (metric of gguf-plugin/test_gluon_kq_gpu.py:81-86).
+Also: determinism, mixed-type layers, the GGUFLinearMethod surface, BASELINE config 1."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ggml_ref as G
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def _x(M, K, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+
+
+def _ref(x, wf):
+    return G.matmul_ref(x.float().cpu().numpy(), wf)
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_gemv_and_gemm_all_types(dev, wt):
+    import gguf_hip
+
+    rng = np.random.default_rng(500 + wt)
+    n, K = 200, 1024
+    raw = G.make_weights(rng, n, K, wt)
+    wf = G.dequantize(raw, wt)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt])
+    worst = 0.0
+    for M in (1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64, 65, 130):
+        x = _x(M, K, 1000 + M, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        torch.cuda.synchronize()
+        assert y.shape == (M, n) and y.dtype == torch.bfloat16
+        yy = y.float().cpu().numpy()
+        assert np.isfinite(yy).all(), (G.NAMES[wt], M)
+        e = G.rel_err(yy, _ref(x, wf))
+        worst = max(worst, e)
+        assert e < TOL, (G.NAMES[wt], M, e)
+        if M in (1, 8, 33):
+            y2 = gguf_hip.mul_mat_grouped(x, gl)
+            assert torch.equal(y, y2), "not deterministic"
+    print(f"{G.NAMES[wt]}: worst rel err {worst:.2e}")
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_gemv_split_k_ragged(dev, wt):
+    """Many k-blocks with several split factors and a ragged row count: every split's partial
+    slice is written (the reference's 0044 bug class, tiles_grouped.py:283-287)."""
+    import gguf_hip
+
+    rng = np.random.default_rng(600 + wt)
+    n, K = 70, 20 * 256
+    raw = G.random_blocks(rng, n, K, wt)
+    wf = G.dequantize(raw, wt)
+    W = torch.from_numpy(raw).to(dev)
+    for target in (1, 3, 7, 40):
+        gl = gguf_hip.pack_layer([W], [n], [wt], target_wgs=target)
+        for M in (1, 7, 32):
+            x = _x(M, K, 2000 + M, dev)
+            e = G.rel_err(gguf_hip.mul_mat_grouped(x, gl).float().cpu().numpy(), _ref(x, wf))
+            assert e < TOL, (G.NAMES[wt], target, M, e)
+
+
+def test_mixed_layer_one_launch(dev):
+    """A merged layer of three types in one grouped launch; with split 1 every shard's columns
+    are bit-identical to its own launch (the reference's mixed-layer identity,
+    gguf-plugin/test_gluon_kq_gpu.py:172-195)."""
+    import gguf_hip
+
+    rng = np.random.default_rng(7)
+    K = 1536
+    shards = [(G.IQ3_S, 70), (G.Q4_K, 128), (G.Q6_K, 100), (G.Q8_0, 64), (G.IQ4_XS, 30)]
+    raws = [G.make_weights(rng, n, K, wt) for wt, n in shards]
+    Ws = [torch.from_numpy(r).to(dev) for r in raws]
+    wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
+    gl = gguf_hip.pack_layer(Ws, [n for _, n in shards], [wt for wt, _ in shards], target_wgs=1)
+    singles = [gguf_hip.pack_layer([W], [n], [wt], target_wgs=1) for W, (wt, n) in zip(Ws, shards)]
+    for M in (1, 6, 20, 40, 200):
+        x = _x(M, K, 3000 + M, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
+        col = 0
+        for s, (wt, n) in zip(singles, shards):
+            ys = gguf_hip.mul_mat_grouped(x, s)
+            assert torch.equal(y[:, col:col + n], ys), (M, G.NAMES[wt])
+            col += n
+
+
+class _WT:
+    def __init__(self, weight_type, shard_weight_type=None):
+        self.weight_type = weight_type
+        self.shard_weight_type = shard_weight_type or {}
+
+
+class _Layer(torch.nn.Module):
+    pass
+
+
+def test_linear_method_mixed_and_single(dev):
+    """GGUFLinearMethod.apply on a mixed-type merged qkv layer (gguf_shards) and on a
+    single-type merged gate/up layer (one concatenated weight), with bias; M = 0 is empty."""
+    import gguf_hip
+
+    rng = np.random.default_rng(8)
+    K = 1024
+    # mixed qkv: shards kept as their own tensors (gguf-plugin/patches/gguf-shard-tensors.patch)
+    types = {"q": G.Q5_K, "k": G.IQ4_NL, "v": G.Q6_K}
+    ns = {"q": 256, "k": 64, "v": 64}
+    raws = {i: G.make_weights(rng, ns[i], K, types[i]) for i in "qkv"}
+    layer = _Layer()
+    layer.weight = torch.nn.Parameter(torch.empty(0, dtype=torch.uint8, device=dev), requires_grad=False)
+    layer.weight.shard_id = ["k", "q", "v"]
+    layer.weight_type = _WT(G.Q4_K, dict(types))
+    layer.gguf_shards = {i: torch.from_numpy(raws[i]).to(dev) for i in ("k", "v", "q")}
+    method = gguf_hip.GGUFLinearMethod()
+    method.process_weights_after_loading(layer)
+    assert list(layer.gguf_groups) == ["q"] and all(layer.gguf_shards[i].numel() == 0 for i in "qkv")
+    wf = np.concatenate([G.dequantize(raws[i], types[i]) for i in "qkv"])
+    bias = torch.randn(384, device=dev).to(torch.bfloat16)
+    for M in (1, 8, 33):
+        x = _x(M, K, 4000 + M, dev)
+        y = method.apply(layer, x, bias)
+        ref = _ref(x, wf) + bias.float().cpu().numpy()[None]
+        assert y.shape == (M, 384) and G.rel_err(y.float().cpu().numpy(), ref) < TOL
+    assert method.apply(layer, torch.empty(0, K, dtype=torch.bfloat16, device=dev)).shape == (0, 384)
+
+    # single-type merged layer: the whole weight, shard offsets as the plugin records them
+    raw_g = G.make_weights(rng, 200, K, G.Q4_K)
+    raw_u = G.make_weights(rng, 200, K, G.Q4_K)
+    layer2 = _Layer()
+    w = torch.from_numpy(np.concatenate([raw_g, raw_u])).to(dev)
+    layer2.weight = torch.nn.Parameter(w, requires_grad=False)
+    layer2.weight.shard_id = [0, 1]
+    layer2.weight.shard_offset_map = {0: (0, 200, raw_g.shape[1]), 1: (200, 400, raw_u.shape[1])}
+    layer2.weight_type = _WT(G.Q4_K, {0: G.Q4_K, 1: G.Q4_K})
+    method.process_weights_after_loading(layer2)
+    assert "__all__" in layer2.gguf_groups and layer2.weight.numel() == 0
+    wf2 = np.concatenate([G.dequantize(raw_g, G.Q4_K), G.dequantize(raw_u, G.Q4_K)])
+    for M in (3, 100):
+        x = _x(M, K, 5000 + M, dev)
+        assert G.rel_err(method.apply(layer2, x).float().cpu().numpy(), _ref(x, wf2)) < TOL
+
+
+def test_raw_rows_op_and_errors(dev):
+    import gguf_hip
+
+    rng = np.random.default_rng(9)
+    raw = G.make_weights(rng, 96, 512, G.Q3_K)
+    x = _x(4, 512, 9, dev)
+    y = gguf_hip.fused_mul_mat_gguf(x, torch.from_numpy(raw).to(dev), G.Q3_K)
+    assert G.rel_err(y.float().cpu().numpy(), _ref(x, G.dequantize(raw, G.Q3_K))) < TOL
+    with pytest.raises(NotImplementedError):
+        gguf_hip.fused_mul_mat_gguf(x, torch.zeros((4, 66 * 2), dtype=torch.uint8, device=dev), 16)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [96], [G.Q3_K])
+    with pytest.raises(ValueError):
+        gguf_hip.mul_mat_grouped(_x(2, 768, 1, dev), gl)       # K mismatch
+
+
+def test_baseline_config1_q8_0(dev):
+    """W[4096, 4096] ~ N(0, 0.02) -> Q8_0 (d = absmax / 127), x[1, 4096] bf16
+    ~ N(0, 1); dequant bit-exact, y within 1e-2."""
+    import gguf_hip
+
+    rng = np.random.default_rng(1)
+    N = K = 4096
+    W = rng.normal(0.0, 0.02, size=(N, K)).astype(np.float32)
+    raw = G.quantize(W, G.Q8_0)
+    wf = G.dequantize(raw, G.Q8_0)
+    Wd = torch.from_numpy(raw).to(dev)
+    got = gguf_hip.dequantize(Wd, G.Q8_0, (N, K)).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), wf.view(np.uint32))
+    x = torch.from_numpy(rng.normal(0, 1, size=(1, K)).astype(np.float32)).to(torch.bfloat16).to(dev)
+    gl = gguf_hip.pack_layer([Wd], [N], [G.Q8_0])
+    e = G.rel_err(gguf_hip.mul_mat_grouped(x, gl).float().cpu().numpy(), _ref(x, wf))
+    assert e < TOL, e
