@@ -167,8 +167,17 @@ template <> __device__ void deq32<GQK_IQ3_S>(const uint8_t* rec, int g, float* w
 
 template <typename O> __device__ __forceinline__ O cvt_out(float v);
 template <> __device__ __forceinline__ float cvt_out<float>(float v) { return v; }
-template <> __device__ __forceinline__ __bf16 cvt_out<__bf16>(float v) { return (__bf16)v; }
-template <> __device__ __forceinline__ _Float16 cvt_out<_Float16>(float v) { return (_Float16)v; }
+// The fp32 value is made opaque before the narrowing conversion: otherwise the compiler may fuse
+// the last multiply into the conversion (v_fma_mixlo_f16(a, b, +0)), which turns a -0.0 product
+// (negative scale x zero quant, kept by gguf-py) into +0.0.
+template <> __device__ __forceinline__ __bf16 cvt_out<__bf16>(float v) {
+  asm volatile("" : "+v"(v));
+  return (__bf16)v;
+}
+template <> __device__ __forceinline__ _Float16 cvt_out<_Float16>(float v) {
+  asm volatile("" : "+v"(v));
+  return (_Float16)v;
+}
 
 // One thread per (row, group of 32 weights).
 template <int T, typename O>
