@@ -34,6 +34,9 @@ int check_launch(const char* what) {
 // 256-CU MI355X, so every SIMD holds four waves streaming weights.
 constexpr int kDefaultTargetWgs = 1024;
 
+// bytes of the split-K arrival counters of `tiles` tiles (rounded to 256 so the partials stay aligned)
+int64_t gqk_counter_bytes(int64_t tiles) { return (tiles * 4 + 255) / 256 * 256; }
+
 }  // namespace
 
 extern "C" {
@@ -52,11 +55,12 @@ int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes) {
   info[3] = t->nplanes;
   if (planes)
     for (int p = 0; p < t->nplanes; ++p) {
-      planes[5 * p + 0] = t->planes[p].size;
-      planes[5 * p + 1] = t->planes[p].nseg;
-      planes[5 * p + 2] = t->planes[p].seg_off;
-      planes[5 * p + 3] = t->planes[p].seg_len;
-      planes[5 * p + 4] = t->planes[p].seg_stride;
+      planes[6 * p + 0] = t->planes[p].size;
+      planes[6 * p + 1] = t->planes[p].nseg;
+      planes[6 * p + 2] = t->planes[p].seg_off;
+      planes[6 * p + 3] = t->planes[p].seg_len;
+      planes[6 * p + 4] = t->planes[p].seg_stride;
+      planes[6 * p + 5] = gqk_col_width(t->planes[p].size);
     }
   return GQK_OK;
 }
@@ -139,7 +143,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   pi.nb = (int32_t)nb;
   pi.n_total = n_total;
   std::vector<int32_t> rows;
-  auto row = [&](int i, int64_t tile0, int ntiles, int64_t kb0, int64_t kb1, int split, int64_t col0) {
+  auto row = [&](int i, int64_t tile0, int ntiles, int64_t kb0, int64_t kb1, int split, int64_t col0, int64_t ctr) {
     int32_t r[GQK_DESC_WORDS] = {0};
     r[D_TYPE] = shards[i].ggml_type;
     r[D_OFF_LO] = (int32_t)(uint32_t)(shards[i].offset & 0xFFFFFFFF);
@@ -152,27 +156,34 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     r[D_COL0] = (int32_t)(col0 + tile0 * 64);
     r[D_NVALID] = (int32_t)std::min<int64_t>((int64_t)ntiles * 64, shards[i].n - tile0 * 64);
     r[D_NB] = (int32_t)nb;
+    r[D_CTR] = (int32_t)ctr;
     rows.insert(rows.end(), r, r + GQK_DESC_WORDS);
   };
+  int64_t tiles = 0;
+  for (int i = 0; i < nshards; ++i) tiles += (shards[i].n + 63) / 64;
   if (M <= 32) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
     pi.m_max = 4 * pi.g;
-    int64_t w0 = 0;
-    for (int i = 0; i < nshards; ++i) w0 += ((shards[i].n + 63) / 64 + 3) / 4;
+    // one workgroup per (tile, k-range), its four waves taking quarters of the k-range: enough
+    // workgroups to fill the chip, each wave keeping >= 2 super-blocks where the shape allows
     const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWgs;
-    int64_t split = (target + w0 - 1) / w0;
-    split = std::max<int64_t>(1, std::min<int64_t>(split, std::max<int64_t>(1, nb / 2)));
+    int64_t split = (target + tiles - 1) / tiles;
+    int64_t cap = std::max<int64_t>(1, nb / 8);
+    if (tiles * cap < 512) cap = std::max<int64_t>(1, nb / 4);
+    split = std::max<int64_t>(1, std::min(split, cap));
     pi.split = (int32_t)split;
-    int64_t col0 = 0;
+    int64_t col0 = 0, ctr = 0;
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
-      for (int64_t t0 = 0; t0 < ntile; t0 += 4)
+      for (int64_t t0 = 0; t0 < ntile; ++t0, ++ctr)
         for (int64_t s = 0; s < split; ++s)   // balanced partition: every split owns >= 1 super-block
-          row(i, t0, (int)std::min<int64_t>(4, ntile - t0), s * nb / split, (s + 1) * nb / split, (int)s, col0);
+          row(i, t0, 1, s * nb / split, (s + 1) * nb / split, (int)s, col0, ctr);
       col0 += shards[i].n;
     }
-    pi.workspace_bytes = split > 1 ? (int64_t)split * pi.m_max * n_total * 4 : 0;
+    // workspace: tile arrival counters (zero before the first launch, left zero by each launch),
+    // then the fp32 partials [split][M][n_total]
+    pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + (int64_t)split * pi.m_max * n_total * 4 : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
     pi.bm = M <= 64 ? 64 : 128;
@@ -181,7 +192,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     int64_t col0 = 0;
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
-      for (int64_t t0 = 0; t0 < ntile; t0 += 2) row(i, t0, (int)std::min<int64_t>(2, ntile - t0), 0, nb, 0, col0);
+      for (int64_t t0 = 0; t0 < ntile; t0 += 2) row(i, t0, (int)std::min<int64_t>(2, ntile - t0), 0, nb, 0, col0, 0);
       col0 += shards[i].n;
     }
     pi.workspace_bytes = 0;
@@ -212,13 +223,21 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
   if (info->form == GQK_FORM_GEMV) {
     if (M > info->m_max) return fail(GQK_ERR_FORM, "linear: M=%d above the GEMV plan's %d rows", M, info->m_max);
     if (info->g != 1 && info->g != 2 && info->g != 4 && info->g != 8) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
+    int64_t tiles = 0;
+    int* counters = nullptr;
+    float* partials = nullptr;
     if (info->split > 1) {
-      int64_t need = (int64_t)info->split * M * info->n_total * 4;
+      tiles = info->n_desc / info->split;   // one descriptor row per (tile, split)
+      const int64_t cb = gqk_counter_bytes(tiles);
+      const int64_t need = cb + (int64_t)info->split * M * info->n_total * 4;
       if (!workspace || workspace_bytes < need)
         return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);
+      if ((uintptr_t)workspace & 255) return fail(GQK_ERR_SHAPE, "linear: workspace not 256-byte aligned");
+      counters = (int*)workspace;
+      partials = (float*)((char*)workspace + cb);
     }
     int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, y,
-                              ldy, (float*)workspace, info->split, info->n_total, (hipStream_t)stream);
+                              ldy, partials, counters, info->split, info->n_total, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }

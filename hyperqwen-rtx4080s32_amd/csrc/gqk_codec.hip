@@ -252,15 +252,17 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
   const uint8_t* rrec = (TO_TILES ? src : dst) + row * stride + kb * rec;
   int poff = 0;
   for (int p = 0; p < pa.nplanes; ++p) {
-    uint8_t* tp = tbase + 64 * poff + r * pa.size[p];
+    const int W = gqk_col_width(pa.size[p]);
+    uint8_t* tp = tbase + 64 * poff + r * W;     // byte j of the row: tp + (j / W) * 64 * W + j % W
     int j = 0;
     for (int sgi = 0; sgi < pa.nseg[p]; ++sgi) {
       int so = pa.seg_off[p] + sgi * pa.seg_stride[p];
       for (int b = 0; b < pa.seg_len[p]; ++b, ++j) {
+        uint8_t* tj = tp + (j / W) * 64 * W + j % W;
         if (TO_TILES)
-          tp[j] = valid ? rrec[so + b] : (uint8_t)0;
+          *tj = valid ? rrec[so + b] : (uint8_t)0;
         else if (valid)
-          ((uint8_t*)rrec)[so + b] = tp[j];
+          ((uint8_t*)rrec)[so + b] = *tj;
       }
     }
     poff += pa.size[p];

@@ -12,9 +12,10 @@
 // The bytes of (tile t, super-block kb) form one contiguous chunk of 64 * REC bytes at
 //     chunk(t, kb) = base + (t * nb + kb) * 64 * REC
 // Inside a chunk the record is split into planes (quants, high bits, scales, d ...); plane p
-// holds the p-th slice of all 64 rows back to back:
-//     byte j of plane p of row r  at  chunk + 64 * plane_off[p] + r * plane_size[p] + j
-// so a wavefront whose lane r reads row r issues one fully coalesced load per plane slice
+// holds the p-th slice of all 64 rows, column-major in columns of W bytes (W = 16, or the
+// largest power of two dividing the plane's bytes per row):
+//     byte j of plane p of row r  at  chunk + 64 * plane_off[p] + ((j / W) * 64 + r) * W + j % W
+// so a wavefront whose lane r reads row r issues one fully coalesced load per column
 // (1 KiB per 16-byte load).  The layout holds exactly the GGUF bytes (no padding inside a
 // chunk; rows past n are zero), which is why bandwidth is counted on raw block bytes.
 #pragma once
@@ -65,6 +66,11 @@ struct gqk_type {
   X(GQK_IQ4_NL, 32, 18,  144, 2, {{128, 8, 2, 16, 18}, {16, 8, 0, 2, 18}})                            \
   X(GQK_IQ3_S, 256, 110, 110, 5, {{64, 1, 2, 64, 0}, {32, 1, 74, 32, 0}, {8, 1, 66, 8, 0}, {4, 1, 106, 4, 0}, {2, 1, 0, 2, 0}}) \
   X(GQK_IQ4_XS, 256, 136, 136, 2, {{128, 1, 8, 128, 0}, {8, 1, 0, 8, 0}})
+
+// Column width of a plane of `size` bytes per row: 16, or the largest power of two dividing it.
+__host__ __device__ constexpr int gqk_col_width(int size) {
+  return size % 16 == 0 ? 16 : size % 8 == 0 ? 8 : size % 4 == 0 ? 4 : size % 2 == 0 ? 2 : 1;
+}
 
 // Host lookup of a type's table entry (nullptr for an unsupported id).
 inline const gqk_type* gqk_type_get(int id) {
@@ -117,6 +123,7 @@ enum {
   D_COL0 = 8,     // output column of the first row of tile D_TILE0
   D_NVALID = 9,   // valid output rows from D_COL0 (the shard's last tile is partial)
   D_NB = 10,      // super-blocks per row (K / 256)
+  D_CTR = 11,     // GEMV split-K: arrival counter of the row's tile (index into the counters)
 };
 
 // forms of a grouped launch

@@ -50,13 +50,16 @@ __device__ __forceinline__ void gld(uint32_t* dst, const uint8_t* p) {
   }
 }
 
+// 16-byte column `col` of row r in a plane with 16-byte columns (column-major: (col * 64 + r) * 16)
+__device__ __forceinline__ const uint8_t* col16(const uint8_t* plane, int r, int col) { return plane + (col * 64 + r) * 16; }
+
 // Per-type decode of one group of 32 consecutive weights (g = 0..7 of a super-block) of row r
 // to 16 dwords of bf16 pairs in natural k order.  load() issues the global loads, out() decodes.
 template <int T> struct GDec;
 
 template <> struct GDec<GQK_Q4_0> {
   uint32_t qs[4], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, c + r * 128 + 16 * g); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
+  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, g)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
   __device__ void out(uint32_t* o) const {
     float dd = g_h2f(d);
 #pragma unroll
@@ -70,7 +73,7 @@ template <> struct GDec<GQK_Q4_0> {
 
 template <> struct GDec<GQK_IQ4_NL> {
   uint32_t qs[4], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, c + r * 128 + 16 * g); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
+  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, g)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
   __device__ void out(uint32_t* o) const {
     float dd = g_h2f(d);
 #pragma unroll
@@ -85,7 +88,7 @@ template <> struct GDec<GQK_IQ4_NL> {
 template <> struct GDec<GQK_Q5_0> {
   uint32_t qs[4], qh, d;
   __device__ void load(const uint8_t* c, int r, int g) {
-    gld<16>(qs, c + r * 128 + 16 * g); gld<4>(&qh, c + 64 * 128 + r * 32 + 4 * g); gld<2>(&d, c + 64 * 160 + r * 16 + 2 * g);
+    gld<16>(qs, col16(c, r, g)); gld<4>(&qh, col16(c + 64 * 128, r, g >> 2) + 4 * (g & 3)); gld<2>(&d, c + 64 * 160 + r * 16 + 2 * g);
   }
   __device__ void out(uint32_t* o) const {
     float dd = g_h2f(d);
@@ -102,7 +105,7 @@ template <> struct GDec<GQK_Q5_0> {
 
 template <> struct GDec<GQK_Q8_0> {
   uint32_t qs[8], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<32>(qs, c + r * 256 + 32 * g); gld<2>(&d, c + 64 * 256 + r * 16 + 2 * g); }
+  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, 2 * g)); gld<16>(qs + 4, col16(c, r, 2 * g + 1)); gld<2>(&d, c + 64 * 256 + r * 16 + 2 * g); }
   __device__ void out(uint32_t* o) const {
     float dd = g_h2f(d);
 #pragma unroll
@@ -117,7 +120,8 @@ template <> struct GDec<GQK_Q2_K> {
   __device__ void load(const uint8_t* c, int r, int g) {
     int h = g >> 2;
     t = g & 3;
-    gld<32>(qs, c + r * 64 + 32 * h);
+    gld<16>(qs, col16(c, r, 2 * h));
+    gld<16>(qs + 4, col16(c, r, 2 * h + 1));
     gld<2>(&sc, c + 64 * 64 + r * 16 + 2 * g);
     gld<4>(&dd, c + 64 * 80 + r * 4);
   }
@@ -143,9 +147,12 @@ template <> struct GDec<GQK_Q3_K> {
   int g;
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
-    gld<32>(qs, c + r * 64 + 32 * (g >> 2));
-    gld<32>(hm, c + 64 * 64 + r * 32);
-    gld<12>(sb, c + 64 * 96 + r * 12);
+    gld<16>(qs, col16(c, r, 2 * (g >> 2)));
+    gld<16>(qs + 4, col16(c, r, 2 * (g >> 2) + 1));
+    gld<16>(hm, col16(c + 64 * 64, r, 0));
+    gld<16>(hm + 4, col16(c + 64 * 64, r, 1));
+    const uint32_t* p = (const uint32_t*)(c + 64 * 96);   // three 4-byte columns
+    sb[0] = p[r]; sb[1] = p[64 + r]; sb[2] = p[128 + r];
     gld<2>(&d, c + 64 * 108 + r * 2);
   }
   __device__ void out(uint32_t* o) const {
@@ -183,7 +190,8 @@ template <> struct GDec<GQK_Q4_K> {
   int g;
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
-    gld<32>(qs, c + r * 128 + 32 * (g >> 1));
+    gld<16>(qs, col16(c, r, 2 * (g >> 1)));
+    gld<16>(qs + 4, col16(c, r, 2 * (g >> 1) + 1));
     gld<16>(hdr, c + 64 * 128 + r * 16);
   }
   __device__ void out(uint32_t* o) const {
@@ -202,8 +210,10 @@ template <> struct GDec<GQK_Q5_K> {
   int g;
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
-    gld<32>(qs, c + r * 128 + 32 * (g >> 1));
-    gld<32>(qh, c + 64 * 128 + r * 32);
+    gld<16>(qs, col16(c, r, 2 * (g >> 1)));
+    gld<16>(qs + 4, col16(c, r, 2 * (g >> 1) + 1));
+    gld<16>(qh, col16(c + 64 * 128, r, 0));
+    gld<16>(qh + 4, col16(c + 64 * 128, r, 1));
     gld<16>(hdr, c + 64 * 160 + r * 16);
   }
   __device__ void out(uint32_t* o) const {
@@ -226,8 +236,10 @@ template <> struct GDec<GQK_Q6_K> {
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
     int h = g >> 2, t = g & 3;
-    gld<32>(ql, c + r * 128 + 64 * h + 32 * (t & 1));
-    gld<32>(qh, c + 64 * 128 + r * 64 + 32 * h);
+    gld<16>(ql, col16(c, r, 4 * h + 2 * (t & 1)));
+    gld<16>(ql + 4, col16(c, r, 4 * h + 2 * (t & 1) + 1));
+    gld<16>(qh, col16(c + 64 * 128, r, 2 * h));
+    gld<16>(qh + 4, col16(c + 64 * 128, r, 2 * h + 1));
     gld<2>(&sc, c + 64 * 192 + r * 16 + 2 * g);
     gld<2>(&d, c + 64 * 208 + r * 2);
   }
@@ -253,7 +265,7 @@ template <> struct GDec<GQK_IQ4_XS> {
   int g;
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
-    gld<16>(qs, c + r * 128 + 16 * g);
+    gld<16>(qs, col16(c, r, g));
     gld<8>(hdr, c + 64 * 128 + r * 8);
   }
   __device__ void out(uint32_t* o) const {
@@ -273,8 +285,8 @@ template <> struct GDec<GQK_IQ3_S> {
   int g;
   __device__ void load(const uint8_t* c, int r, int g_) {
     g = g_;
-    gld<8>(qs, c + r * 64 + 8 * g);
-    gld<4>(&sg, c + 64 * 64 + r * 32 + 4 * g);
+    gld<8>(qs, col16(c, r, g >> 1) + 8 * (g & 1));
+    gld<4>(&sg, col16(c + 64 * 64, r, g >> 2) + 4 * (g & 3));
     gld<8>(qh, c + 64 * 96 + r * 8);
     gld<4>(&scb, c + 64 * 104 + r * 4);
     gld<2>(&d, c + 64 * 108 + r * 2);

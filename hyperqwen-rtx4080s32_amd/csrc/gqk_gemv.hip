@@ -5,24 +5,28 @@
 // gluon_mul_mat_tiles_grouped, gguf-plugin/gluon/interface.py:169-182), with bf16 activations
 // in place of its int8 ones.
 //
-// Work split.  One workgroup (4 waves) per descriptor row: the row names a shard, up to four
-// consecutive 64-row tiles of it (one per wave) and a k-range of 256-weight super-blocks.  The
-// type is uniform per workgroup.  Lane r of a wave owns weight row r of its tile and streams
-// that row's record planes with 16-byte loads (one coalesced 1 KiB access per plane slice).
+// Work split.  One workgroup (4 waves) per descriptor row: the row names a shard, one 64-row
+// tile of it and a k-range of 256-weight super-blocks, which the four waves split into
+// quarters.  The type is uniform per workgroup.  Lane r of a wave owns weight row r of the tile
+// and streams that row's record planes with 16-byte loads (one coalesced 1 KiB access per plane
+// column); each wave stages its own slice of x in a private LDS region, so the main loop has no
+// workgroup barrier.
 //
 // Arithmetic.  Every format's weight is w = d * sc * q - dmin * m with q a small integer.  The
 // lane decodes q + c (c = 128, or 0 for the table formats) straight into bf16 bit patterns
 // (0x4300 | u is exactly 128 + u for u < 128; table formats look up exact bf16 values) and
 // feeds them as the B operand of v_mfma_f32_4x4x4_16b_bf16 (16 blocks of 4 weight rows x 4
 // tokens x 4 k).  One chain of MFMAs covers one scale group (16 or 32 weights); the epilogue
-// applies it in fp32:  y += (d * sc) * C - (c * d * sc + dmin * m) * sum(x over the group).
+// applies it in fp32:  y += (d * sc) * C - (c * d * sc + dmin * m) * sum(x over the group), the
+// second term as one v_mfma_f32_4x4x1f32 outer product (token sums x row biases) per group.
 // The group sums of x are computed once per workgroup when x is staged into LDS.  Products
 // bf16 x exact-integer are exact in the MFMA, accumulation is fp32, so the result equals an
 // fp32 matmul of the gguf-py weights up to summation order.
 //
 // Split-K: with more than one k-range per tile the workgroups write fp32 partials
-// [split][M][n_total] that gemv_reduce sums in a fixed order (deterministic), as the
-// reference's sum_partials does (gguf-plugin/gluon/tiles_grouped.py:142-162).
+// [split][M][n_total]; the last workgroup of a tile to arrive sums them in split order
+// (deterministic, one rounding to bf16), the reference's sum_partials
+// (gguf-plugin/gluon/tiles_grouped.py:142-162) fused into the same launch.
 #include <hip/hip_runtime.h>
 #include "gqk_common.h"
 #include "gqk_internal.h"
@@ -32,7 +36,6 @@ namespace gqk {
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-#define MAGIC 0x43004300u   // bf16 128.0 in both halves
 
 enum { FAM_NAT = 0, FAM_SWAP = 1, FAM_IQ4 = 2 };
 
@@ -54,11 +57,31 @@ __device__ __forceinline__ uint32_t bf16x2(float lo, float hi) {
 }
 __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int b) { return (w[b >> 2] >> (8 * (b & 3))) & 0xFF; }
 
+// Opaque constants for the decode: gfx9 VOP3 takes no literal, so with the masks held in SGPRs
+// and the bf16 exponent pattern (0x4300 = 128.0 in each half) in a VGPR, (a & m) | o is a single
+// v_and_or_b32.  The values are hidden from constant folding by empty asm statements (no
+// instruction is emitted), so the compiler still schedules the ALU ops and their MFMA hazards.
+struct Masks {
+  uint32_t f, ff, t3, mg;   // 0x000F000F, 0x00FF00FF, 0x00030003 (SGPRs); 0x43004300 (VGPR)
+};
+__device__ __forceinline__ Masks make_masks() {
+  Masks k{0x000F000Fu, 0x00FF00FFu, 0x00030003u, 0x43004300u};
+  asm volatile("" : "+s"(k.f));
+  asm volatile("" : "+s"(k.ff));
+  asm volatile("" : "+s"(k.t3));
+  asm volatile("" : "+v"(k.mg));
+  return k;
+}
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
+
+// Row r's slice of a plane of N bytes per row (N a multiple of 16).  Planes are column-major in
+// 16-byte columns: column i of row r sits at (i * 64 + r) * 16, so load i of a wave is one
+// contiguous 1 KiB access.
 template <int N>
-__device__ __forceinline__ void ld16(uint32_t* dst, const uint8_t* p) {
+__device__ __forceinline__ void ldp(uint32_t* dst, const uint8_t* plane, int r) {
 #pragma unroll
   for (int i = 0; i < N / 16; ++i) {
-    uint4 v = *(const uint4*)(p + 16 * i);
+    uint4 v = *(const uint4*)(plane + (i * 64 + r) * 16);
     dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
   }
 }
@@ -71,13 +94,13 @@ template <int T> struct Dec;
 template <> struct Dec<GQK_Q4_0> {
   static constexpr int SUB = 32, FAM = FAM_SWAP, REC = 144;
   uint32_t qs[32], dw[4];
-  __device__ void load(const uint8_t* c, int r) { ld16<128>(qs, c + r * 128); ld16<16>(dw, c + 64 * 128 + r * 16); }
+  __device__ void load(const uint8_t* c, int r) { ldp<128>(qs, c, r); ldp<16>(dw, c + 64 * 128, r); }
   __device__ void scales(int s, float& sc, float& b) const { float d = h2f(dw[s >> 1] >> (16 * (s & 1))); sc = d; b = 136.f * d; }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = qs[4 * s + (m & 3)];
     if (m >= 4) w >>= 4;
-    b0 = (w & 0x000F000Fu) | MAGIC;
-    b1 = ((w >> 8) & 0x000F000Fu) | MAGIC;
+    b0 = and_or(w, k.f, k.mg);
+    b1 = and_or(w >> 8, k.f, k.mg);
   }
 };
 
@@ -85,26 +108,26 @@ template <> struct Dec<GQK_Q5_0> {
   static constexpr int SUB = 32, FAM = FAM_SWAP, REC = 176;
   uint32_t qs[32], qh[8], dw[4];
   __device__ void load(const uint8_t* c, int r) {
-    ld16<128>(qs, c + r * 128); ld16<32>(qh, c + 64 * 128 + r * 32); ld16<16>(dw, c + 64 * 160 + r * 16);
+    ldp<128>(qs, c, r); ldp<32>(qh, c + 64 * 128, r); ldp<16>(dw, c + 64 * 160, r);
   }
   __device__ void scales(int s, float& sc, float& b) const { float d = h2f(dw[s >> 1] >> (16 * (s & 1))); sc = d; b = 144.f * d; }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = qs[4 * s + (m & 3)];
     if (m >= 4) w >>= 4;
     uint32_t h4 = (qh[s] >> (4 * m)) & 0xFu;
     uint32_t hb = ((h4 * 0x00204081u) & 0x01010101u) << 4;   // bit i of h4 -> bit 4 of byte i
     uint32_t u = (w & 0x0F0F0F0Fu) | hb;
-    b0 = (u & 0x00FF00FFu) | MAGIC;
-    b1 = ((u >> 8) & 0x00FF00FFu) | MAGIC;
+    b0 = and_or(u, k.ff, k.mg);
+    b1 = and_or(u >> 8, k.ff, k.mg);
   }
 };
 
 template <> struct Dec<GQK_Q8_0> {
   static constexpr int SUB = 32, FAM = FAM_NAT, REC = 272;
   uint32_t qs[64], dw[4];
-  __device__ void load(const uint8_t* c, int r) { ld16<256>(qs, c + r * 256); ld16<16>(dw, c + 64 * 256 + r * 16); }
+  __device__ void load(const uint8_t* c, int r) { ldp<256>(qs, c, r); ldp<16>(dw, c + 64 * 256, r); }
   __device__ void scales(int s, float& sc, float& b) const { float d = h2f(dw[s >> 1] >> (16 * (s & 1))); sc = d; b = 128.f * d; }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = qs[8 * s + m] ^ 0x80808080u;   // int8 q -> q + 128 as unsigned bytes
     b0 = bf16x2((float)(w & 0xFF), (float)((w >> 8) & 0xFF));
     b1 = bf16x2((float)((w >> 16) & 0xFF), (float)(w >> 24));
@@ -115,7 +138,7 @@ template <> struct Dec<GQK_Q2_K> {
   static constexpr int SUB = 16, FAM = FAM_SWAP, REC = 84;
   uint32_t qs[16], sc[4], dd;
   __device__ void load(const uint8_t* c, int r) {
-    ld16<64>(qs, c + r * 64); ld16<16>(sc, c + 64 * 64 + r * 16); dd = *(const uint32_t*)(c + 64 * 80 + r * 4);
+    ldp<64>(qs, c, r); ldp<16>(sc, c + 64 * 64, r); dd = *(const uint32_t*)(c + 64 * 80 + r * 4);
   }
   __device__ void scales(int s, float& scale, float& b) const {
     uint32_t sb = byte_of(sc, s);
@@ -123,11 +146,11 @@ template <> struct Dec<GQK_Q2_K> {
     scale = d * (float)(sb & 0xF);
     b = 128.f * scale + dmin * (float)(sb >> 4);
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int h = s >> 3, t = (s >> 1) & 3, hf = s & 1;
     uint32_t w = qs[8 * h + 4 * hf + m] >> (2 * t);
-    b0 = (w & 0x00030003u) | MAGIC;
-    b1 = ((w >> 8) & 0x00030003u) | MAGIC;
+    b0 = and_or(w, k.t3, k.mg);
+    b1 = and_or(w >> 8, k.t3, k.mg);
   }
 };
 
@@ -135,10 +158,10 @@ template <> struct Dec<GQK_Q3_K> {
   static constexpr int SUB = 16, FAM = FAM_SWAP, REC = 110;
   uint32_t qs[16], hm[8], sb[3], d16;
   __device__ void load(const uint8_t* c, int r) {
-    ld16<64>(qs, c + r * 64);
-    ld16<32>(hm, c + 64 * 64 + r * 32);
-    const uint32_t* p = (const uint32_t*)(c + 64 * 96 + r * 12);
-    sb[0] = p[0]; sb[1] = p[1]; sb[2] = p[2];
+    ldp<64>(qs, c, r);
+    ldp<32>(hm, c + 64 * 64, r);
+    const uint32_t* p = (const uint32_t*)(c + 64 * 96);   // 12-byte plane: three 4-byte columns
+    sb[0] = p[r]; sb[1] = p[64 + r]; sb[2] = p[128 + r];
     d16 = *(const uint16_t*)(c + 64 * 108 + r * 2);
   }
   __device__ void scales(int s, float& scale, float& b) const {
@@ -147,13 +170,13 @@ template <> struct Dec<GQK_Q3_K> {
     scale = h2f(d16) * (float)((lo | (hi << 4)) - 32);
     b = 132.f * scale;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int n = s >> 3, j = (s >> 1) & 3, hf = s & 1;
     uint32_t q = (qs[8 * n + 4 * hf + m] >> (2 * j)) & 0x03030303u;
     uint32_t h = (hm[4 * hf + m] >> (4 * n + j)) & 0x01010101u;
     uint32_t u = q | (h << 2);
-    b0 = (u & 0x00FF00FFu) | MAGIC;
-    b1 = ((u >> 8) & 0x00FF00FFu) | MAGIC;
+    b0 = and_or(u, k.ff, k.mg);
+    b1 = and_or(u >> 8, k.ff, k.mg);
   }
 };
 
@@ -170,17 +193,17 @@ __device__ __forceinline__ void scale_min_k4w(const uint32_t* S, int j, int& sc,
 template <> struct Dec<GQK_Q4_K> {
   static constexpr int SUB = 32, FAM = FAM_SWAP, REC = 144;
   uint32_t qs[32], hdr[4];
-  __device__ void load(const uint8_t* c, int r) { ld16<128>(qs, c + r * 128); ld16<16>(hdr, c + 64 * 128 + r * 16); }
+  __device__ void load(const uint8_t* c, int r) { ldp<128>(qs, c, r); ldp<16>(hdr, c + 64 * 128, r); }
   __device__ void scales(int s, float& scale, float& b) const {
     int sc, m;
     scale_min_k4w(hdr + 1, s, sc, m);
     scale = h2f(hdr[0]) * (float)sc;
     b = 128.f * scale + h2f(hdr[0] >> 16) * (float)m;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = qs[8 * (s >> 1) + m] >> (4 * (s & 1));
-    b0 = (w & 0x000F000Fu) | MAGIC;
-    b1 = ((w >> 8) & 0x000F000Fu) | MAGIC;
+    b0 = and_or(w, k.f, k.mg);
+    b1 = and_or(w >> 8, k.f, k.mg);
   }
 };
 
@@ -188,7 +211,7 @@ template <> struct Dec<GQK_Q5_K> {
   static constexpr int SUB = 32, FAM = FAM_SWAP, REC = 176;
   uint32_t qs[32], qh[8], hdr[4];
   __device__ void load(const uint8_t* c, int r) {
-    ld16<128>(qs, c + r * 128); ld16<32>(qh, c + 64 * 128 + r * 32); ld16<16>(hdr, c + 64 * 160 + r * 16);
+    ldp<128>(qs, c, r); ldp<32>(qh, c + 64 * 128, r); ldp<16>(hdr, c + 64 * 160, r);
   }
   __device__ void scales(int s, float& scale, float& b) const {
     int sc, m;
@@ -196,11 +219,11 @@ template <> struct Dec<GQK_Q5_K> {
     scale = h2f(hdr[0]) * (float)sc;
     b = 128.f * scale + h2f(hdr[0] >> 16) * (float)m;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = (qs[8 * (s >> 1) + m] >> (4 * (s & 1))) & 0x0F0F0F0Fu;
     uint32_t u = w | (((qh[m] >> s) & 0x01010101u) << 4);
-    b0 = (u & 0x00FF00FFu) | MAGIC;
-    b1 = ((u >> 8) & 0x00FF00FFu) | MAGIC;
+    b0 = and_or(u, k.ff, k.mg);
+    b1 = and_or(u >> 8, k.ff, k.mg);
   }
 };
 
@@ -208,29 +231,29 @@ template <> struct Dec<GQK_Q6_K> {
   static constexpr int SUB = 16, FAM = FAM_SWAP, REC = 210;
   uint32_t ql[32], qh[16], sc[4], d16;
   __device__ void load(const uint8_t* c, int r) {
-    ld16<128>(ql, c + r * 128); ld16<64>(qh, c + 64 * 128 + r * 64); ld16<16>(sc, c + 64 * 192 + r * 16);
+    ldp<128>(ql, c, r); ldp<64>(qh, c + 64 * 128, r); ldp<16>(sc, c + 64 * 192, r);
     d16 = *(const uint16_t*)(c + 64 * 208 + r * 2);
   }
   __device__ void scales(int s, float& scale, float& b) const {
     scale = h2f(d16) * (float)(int8_t)byte_of(sc, s);
     b = 160.f * scale;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int h = s >> 3, t = (s >> 1) & 3, hf = s & 1;
     uint32_t lo = (ql[16 * h + 8 * (t & 1) + 4 * hf + m] >> (4 * (t >> 1))) & 0x0F0F0F0Fu;
     uint32_t hi = (qh[8 * h + 4 * hf + m] >> (2 * t)) & 0x03030303u;
     uint32_t u = lo | (hi << 4);
-    b0 = (u & 0x00FF00FFu) | MAGIC;
-    b1 = ((u >> 8) & 0x00FF00FFu) | MAGIC;
+    b0 = and_or(u, k.ff, k.mg);
+    b1 = and_or(u >> 8, k.ff, k.mg);
   }
 };
 
 template <> struct Dec<GQK_IQ4_NL> {
   static constexpr int SUB = 32, FAM = FAM_IQ4, REC = 144;
   uint32_t qs[32], dw[4];
-  __device__ void load(const uint8_t* c, int r) { ld16<128>(qs, c + r * 128); ld16<16>(dw, c + 64 * 128 + r * 16); }
+  __device__ void load(const uint8_t* c, int r) { ldp<128>(qs, c, r); ldp<16>(dw, c + 64 * 128, r); }
   __device__ void scales(int s, float& sc, float& b) const { sc = h2f(dw[s >> 1] >> (16 * (s & 1))); b = 0.f; }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb, const Masks&) const {
     uint32_t w = qs[4 * s + (m >> 1)] >> (16 * (m & 1));
     b0 = tb.iq4[w & 0xFF];
     b1 = tb.iq4[(w >> 8) & 0xFF];
@@ -241,7 +264,7 @@ template <> struct Dec<GQK_IQ4_XS> {
   static constexpr int SUB = 32, FAM = FAM_IQ4, REC = 136;
   uint32_t qs[32], hdr[2];
   __device__ void load(const uint8_t* c, int r) {
-    ld16<128>(qs, c + r * 128);
+    ldp<128>(qs, c, r);
     uint2 h = *(const uint2*)(c + 64 * 128 + r * 8);
     hdr[0] = h.x; hdr[1] = h.y;
   }
@@ -250,7 +273,7 @@ template <> struct Dec<GQK_IQ4_XS> {
     sc = h2f(hdr[0]) * (float)(ls - 32);
     b = 0.f;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb, const Masks&) const {
     uint32_t w = qs[4 * s + (m >> 1)] >> (16 * (m & 1));
     b0 = tb.iq4[w & 0xFF];
     b1 = tb.iq4[(w >> 8) & 0xFF];
@@ -261,8 +284,8 @@ template <> struct Dec<GQK_IQ3_S> {
   static constexpr int SUB = 32, FAM = FAM_NAT, REC = 110;
   uint32_t qs[16], sg[8], qh[2], scb, d16;
   __device__ void load(const uint8_t* c, int r) {
-    ld16<64>(qs, c + r * 64);
-    ld16<32>(sg, c + 64 * 64 + r * 32);
+    ldp<64>(qs, c, r);
+    ldp<32>(sg, c + 64 * 64, r);
     uint2 h = *(const uint2*)(c + 64 * 96 + r * 8);
     qh[0] = h.x; qh[1] = h.y;
     scb = *(const uint32_t*)(c + 64 * 104 + r * 4);
@@ -272,7 +295,7 @@ template <> struct Dec<GQK_IQ3_S> {
     sc = h2f(d16) * (float)(1 + 2 * (int)((scb >> (4 * s)) & 0xF));
     b = 0.f;
   }
-  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb) const {
+  __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs& tb, const Masks&) const {
     int l = m >> 1, half = m & 1;
     uint32_t qsb = (qs[2 * s + (l >> 1)] >> (8 * (2 * (l & 1) + half))) & 0xFF;
     uint32_t qhb = byte_of(qh, s);
@@ -284,114 +307,143 @@ template <> struct Dec<GQK_IQ3_S> {
   }
 };
 
-// ---- x staging: slot (k / 4 in the decoder's order) x token, 4 bf16 each.
-// FAM_NAT: slot q holds k = 4q .. 4q+3; FAM_SWAP: (4q, 4q+2, 4q+1, 4q+3);
-// FAM_IQ4: slot q = 8s + m holds (32s + 2m, 32s + 2m + 16, 32s + 2m + 1, 32s + 2m + 17).
+__device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+// ---- x staging: wave-private, one super-block at a time.  An item is (token t, 32-weight group
+// s32): 64 bytes of x loaded with four 16-byte loads, rearranged into the decoder's 8 slots and
+// summed (two 16-sums and their 32-sum for the bias terms).
 template <int FAM>
-__device__ __forceinline__ uint2 stage_slot(const uint16_t* xr, int q) {
-  if (FAM == FAM_IQ4) {
-    int s = q >> 3, m = q & 7;
-    uint32_t a = *(const uint32_t*)(xr + 32 * s + 2 * m);
-    uint32_t c = *(const uint32_t*)(xr + 32 * s + 2 * m + 16);
-    return make_uint2((a & 0xFFFFu) | (c << 16), (a >> 16) | (c & 0xFFFF0000u));
-  } else {
-    uint2 v = *(const uint2*)(xr + 4 * q);
-    if (FAM == FAM_SWAP) {
-      return make_uint2((v.x & 0xFFFFu) | (v.y << 16), (v.x >> 16) | (v.y & 0xFFFF0000u));
+__device__ __forceinline__ void slots_of_group(const uint4 (&v)[4], uint2 (&o)[8]) {
+  const uint32_t w[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                          v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};   // k pairs (2j, 2j+1)
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if (FAM == FAM_NAT) {
+      o[m] = make_uint2(w[2 * m], w[2 * m + 1]);
+    } else if (FAM == FAM_SWAP) {                  // (4m, 4m+2, 4m+1, 4m+3)
+      const uint32_t a = w[2 * m], c = w[2 * m + 1];
+      o[m] = make_uint2((a & 0xFFFFu) | (c << 16), (a >> 16) | (c & 0xFFFF0000u));
+    } else {                                       // (2m, 2m+16, 2m+1, 2m+17)
+      const uint32_t a = w[m], c = w[m + 8];
+      o[m] = make_uint2((a & 0xFFFFu) | (c << 16), (a >> 16) | (c & 0xFFFF0000u));
     }
-    return v;
   }
 }
 
-__device__ __forceinline__ float bf2f(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+template <int MPAD>
+struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16 + 8 group sums x MPAD
+  static constexpr int X = 64 * MPAD * 8;
+  static constexpr int BYTES = X + 24 * MPAD * 4;
+};
 
-// LDS budget: x chunk 16 KiB (CH super-blocks x 64 slots x MPAD tokens x 8 B with CH * MPAD = 32),
-// group sums 3 KiB, tables 9 KiB.
-#define GEMV_XCH_SLOTS 2048   // CH * 64 * MPAD
-#define GEMV_LDS_X (GEMV_XCH_SLOTS * 8)
-#define GEMV_LDS_SUM (32 * 24 * 4)
+// Issue the loads of super-block kb's x items (clamped addresses; masked when written).
+template <int MPAD>
+__device__ __forceinline__ void stage_load(const uint16_t* __restrict__ x, int64_t ldx, int M, int kb, int lane,
+                                           uint4 (&v)[(8 * MPAD + 63) / 64][4]) {
+  constexpr int NI = (8 * MPAD + 63) / 64;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = min(lane + 64 * i, 8 * MPAD - 1), t = it % MPAD, s32 = it / MPAD;
+    const uint4* p = (const uint4*)(x + min(t, M - 1) * ldx + (int64_t)kb * 256 + 32 * s32);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[i][j] = p[j];
+  }
+}
 
-template <int G, int T>
-__device__ __forceinline__ void gemv_tile(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
-                                          const uint16_t* __restrict__ x, int64_t ldx, int M, uint8_t* lds,
-                                          const Tabs& tb, v4f (&acc)[G]) {
-  typedef Dec<T> D;
-  constexpr int MPAD = 4 * G, CH = 32 / MPAD, MPS = D::SUB / 4, NSUB = 256 / D::SUB;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kb0 = dsc[D_KB0], kb1 = dsc[D_KB1], nb = dsc[D_NB];
-  const int ntiles = dsc[D_NTILES];
-  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
-  const int64_t tile = dsc[D_TILE0] + wave;
-  const bool active = wave < ntiles;
-  const uint8_t* tbase = packed + off + tile * nb * (int64_t)(64 * D::REC);
-  uint2* xs = (uint2*)lds;
-  float* xsum16 = (float*)(lds + GEMV_LDS_X);
-  float* xsum32 = xsum16 + CH * 16 * MPAD;
-
-  for (int kc = kb0; kc < kb1; kc += CH) {
-    const int nch = min(CH, kb1 - kc);
-    __syncthreads();
-    // stage x[:, kc*256 .. (kc+nch)*256) in the decoder's slot order, zero for tokens >= M
-    for (int it = tid; it < nch * 64 * MPAD; it += 256) {
-      int t = it % MPAD, q = it / MPAD;   // q = kbl * 64 + slot
-      uint2 v = make_uint2(0, 0);
-      if (t < M) v = stage_slot<D::FAM>(x + t * ldx + (int64_t)(kc + (q >> 6)) * 256, q & 63);
-      xs[it] = v;
-    }
-    for (int it = tid; it < nch * 8 * MPAD; it += 256) {
-      int t = it % MPAD, q = it / MPAD;   // q = kbl * 8 + s32
+template <int MPAD, int FAM>
+__device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const uint4 (&v)[(8 * MPAD + 63) / 64][4]) {
+  constexpr int NI = (8 * MPAD + 63) / 64;
+  uint2* xs = (uint2*)wl;
+  float* xsum16 = (float*)(wl + WaveX<MPAD>::X);
+  float* xsum32 = xsum16 + 16 * MPAD;
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int it = lane + 64 * i, t = it % MPAD, s32 = it / MPAD;
+    if (it < 8 * MPAD) {
+      uint2 o[8];
+      slots_of_group<FAM>(v[i], o);
       float a = 0.f, b = 0.f;
-      if (t < M) {
-        const uint16_t* xr = x + t * ldx + (int64_t)(kc + (q >> 3)) * 256 + 32 * (q & 7);
+      const uint32_t* w = (const uint32_t*)&v[i][0];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) a += bf2f(xr[j]);
+      for (int j = 0; j < 8; ++j) a += bf2f(w[j] & 0xFFFF) + bf2f(w[j] >> 16);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) b += bf2f(xr[16 + j]);
-      }
-      int kbl = q >> 3, s = q & 7;
-      xsum16[(kbl * 16 + 2 * s) * MPAD + t] = a;
-      xsum16[(kbl * 16 + 2 * s + 1) * MPAD + t] = b;
-      xsum32[(kbl * 8 + s) * MPAD + t] = a + b;
+      for (int j = 8; j < 16; ++j) b += bf2f(w[j] & 0xFFFF) + bf2f(w[j] >> 16);
+      const bool live = t < M;
+#pragma unroll
+      for (int m = 0; m < 8; ++m) xs[(s32 * 8 + m) * MPAD + t] = live ? o[m] : make_uint2(0, 0);
+      xsum16[(2 * s32) * MPAD + t] = live ? a : 0.f;
+      xsum16[(2 * s32 + 1) * MPAD + t] = live ? b : 0.f;
+      xsum32[s32 * MPAD + t] = live ? a + b : 0.f;
     }
-    __syncthreads();
-    if (!active) continue;
+  }
+}
 
-    D cur;
-    cur.load(tbase + (int64_t)kc * 64 * D::REC, lane);
-    for (int kbl = 0; kbl < nch; ++kbl) {
-      D nxt;
-      if (kbl + 1 < nch) nxt.load(tbase + (int64_t)(kc + kbl + 1) * 64 * D::REC, lane);
+// One wave: weight rows of tile `tile`, super-blocks [kw0, kw1), accumulating into acc.
+template <int G, int T>
+__device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
+                                          int64_t ldx, int M, int kw0, int kw1, uint8_t* wl, const Tabs& tb,
+                                          const Masks& mk, v4f (&acc)[G]) {
+  typedef Dec<T> D;
+  constexpr int MPAD = 4 * G, MPS = D::SUB / 4, NSUB = 256 / D::SUB, NI = (8 * MPAD + 63) / 64;
+  constexpr bool BIAS = !(T == GQK_IQ4_NL || T == GQK_IQ4_XS || T == GQK_IQ3_S);
+  const int lane = threadIdx.x & 63, li = lane & 3;
+  const uint2* xs = (const uint2*)wl;
+  const float* xsum16 = (const float*)(wl + WaveX<MPAD>::X);
+  const float* xsum32 = xsum16 + 16 * MPAD;
+  if (kw0 >= kw1) return;
+
+  // one record (super-block) of the lane's row: MFMA chains per scale group, fp32 epilogue
+  auto process = [&](const D& rec) {
 #pragma unroll
-      for (int s = 0; s < NSUB; ++s) {
-        float scale, bias;
-        cur.scales(s, scale, bias);
-        v4f C[G];
+    for (int s = 0; s < NSUB; ++s) {
+      float scale, bias;
+      rec.scales(s, scale, bias);
+      v4f C[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) C[g] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < G; ++g) C[g] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int m = 0; m < MPS; ++m) {
-          uint32_t b0, b1;
-          cur.pair(s, m, b0, b1, tb);
-          v4s B = __builtin_bit_cast(v4s, make_uint2(b0, b1));
-          const int slot = s * MPS + m;
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            v4s A = __builtin_bit_cast(v4s, xs[(kbl * 64 + slot) * MPAD + 4 * g + (lane & 3)]);
-            C[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A, B, C[g], 0, 0, 0);
-          }
-        }
-        const float* xsm = (D::SUB == 16 ? xsum16 + (kbl * 16 + s) * MPAD : xsum32 + (kbl * 8 + s) * MPAD);
+      for (int m = 0; m < MPS; ++m) {
+        uint32_t b0, b1;
+        rec.pair(s, m, b0, b1, tb, mk);
+        v4s B = __builtin_bit_cast(v4s, make_uint2(b0, b1));
+        const int slot = s * MPS + m;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          float4 sx = *(const float4*)(xsm + 4 * g);
-          acc[g][0] += scale * C[g][0] - bias * sx.x;
-          acc[g][1] += scale * C[g][1] - bias * sx.y;
-          acc[g][2] += scale * C[g][2] - bias * sx.z;
-          acc[g][3] += scale * C[g][3] - bias * sx.w;
+          v4s A = __builtin_bit_cast(v4s, xs[slot * MPAD + 4 * g + li]);
+          C[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A, B, C[g], 0, 0, 0);
         }
       }
-      cur = nxt;
+      const float* xsm = (D::SUB == 16 ? xsum16 + s * MPAD : xsum32 + s * MPAD);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if constexpr (BIAS) {
+          // acc[i][row] -= sum_x[token i] * bias[row]: an fp32 outer product per 4x4 block
+          acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(xsm[4 * g + li], -bias, acc[g], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[g][i] = __builtin_fmaf(scale, C[g][i], acc[g][i]);
+      }
     }
+  };
+
+  // Straight-line pipeline per super-block: the next super-block's x loads and record loads are
+  // issued before this one is decoded; its x is written to LDS after (waiting for the x loads
+  // only, which precede the record loads), and the record hand-off is the only wait on those.
+  uint4 xv[NI][4];
+  stage_load<MPAD>(x, ldx, M, kw0, lane, xv);
+  D cur;
+  cur.load(tbase + (int64_t)kw0 * 64 * D::REC, lane);
+  stage_store<MPAD, D::FAM>(wl, M, lane, xv);
+  for (int kb = kw0; kb < kw1; ++kb) {
+    D nxt;
+    const bool more = kb + 1 < kw1;
+    if (more) {
+      stage_load<MPAD>(x, ldx, M, kb + 1, lane, xv);
+      nxt.load(tbase + (int64_t)(kb + 1) * 64 * D::REC, lane);
+    }
+    process(cur);
+    if (more) stage_store<MPAD, D::FAM>(wl, M, lane, xv);
+    cur = nxt;
   }
 }
 
@@ -415,93 +467,142 @@ __device__ void build_tables(uint8_t* lds_tab, int type) {
   }
 }
 
+#define GEMV_TAB_BYTES 9216
+
+// LDS of a workgroup: 4 wave-private x regions, then the IQ tables.
+template <int G>
+__host__ __device__ constexpr int gemv_lds_bytes(bool tables) {
+  return 4 * WaveX<4 * G>::BYTES + (tables ? GEMV_TAB_BYTES : 0);
+}
+
+// One workgroup per descriptor row: one 64-row tile, its k-range split over the 4 waves, the
+// waves' sums combined through LDS in a fixed order; with split-K (part != nullptr) the fp32
+// partial goes to part[split] and the last workgroup of the tile to arrive (counter ctr[tile])
+// sums the partials in split order and writes y, then resets the counter.
 template <int G, int ONLY>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
                                                    const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                    uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
-                                                   int64_t n_total) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[GEMV_LDS_X + GEMV_LDS_SUM + 9216];
+                                                   int* __restrict__ ctr, int64_t n_total, int split) {
+  constexpr int MPAD = 4 * G;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[gemv_lds_bytes<G>(true)];
   const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
   const int type = dsc[D_TYPE];
-  uint8_t* lds_tab = lds + GEMV_LDS_X + GEMV_LDS_SUM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint8_t* lds_tab = lds + 4 * WaveX<MPAD>::BYTES;
+  const bool iq = type == GQK_IQ4_NL || type == GQK_IQ4_XS || type == GQK_IQ3_S;
   Tabs tb{(const uint32_t*)lds_tab, (const uint2*)lds_tab, (const uint4*)(lds_tab + 4096)};
-  build_tables(lds_tab, type);   // made visible by the first barrier of the staging loop
+  if (iq) {
+    build_tables(lds_tab, type);
+    __syncthreads();
+  }
+  const Masks mk = make_masks();
+  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
+  const int64_t tile = dsc[D_TILE0];
+  const int nb = dsc[D_NB], kb0 = dsc[D_KB0], nk = dsc[D_KB1] - kb0;
+  const int kw0 = kb0 + (wave * nk) / 4, kw1 = kb0 + ((wave + 1) * nk) / 4;
+  uint8_t* wl = lds + wave * WaveX<MPAD>::BYTES;
   v4f acc[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
 
-#define RUN(T) if ((ONLY == 0 || ONLY == T) && type == T) gemv_tile<G, T>(packed, dsc, x, ldx, M, lds, tb, acc);
+#define RUN(T)                                                                                           \
+  if ((ONLY == 0 || ONLY == T) && type == T)                                                             \
+    gemv_wave<G, T>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, wl, tb, mk, acc);
   RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
   RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (wave >= dsc[D_NTILES]) return;
-  const int r = wave * 64 + lane;
-  if (r >= dsc[D_NVALID]) return;
-  const int64_t col = (int64_t)dsc[D_COL0] + r;
-  if (part == nullptr) {
+  // combine the four waves (fixed order) in wave 0
+  __syncthreads();                                  // every wave is done with its x region
+  v4f* red = (v4f*)lds;                             // [wave][g][lane]
+  if (wave > 0)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) red[(wave * G + g) * 64 + lane] = acc[g];
+  __syncthreads();
+  if (wave > 0) return;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int t = 4 * g + i;
-        if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)acc[g][i]);
-      }
-  } else {
-    float* p = part + (int64_t)dsc[D_SPLIT] * M * n_total;
+  for (int w = 1; w < 4; ++w)
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        int t = 4 * g + i;
-        if (t < M) p[t * n_total + col] = acc[g][i];
-      }
-  }
-}
+    for (int g = 0; g < G; ++g) acc[g] += red[(w * G + g) * 64 + lane];
 
-// y[t, c] = bf16( sum_s part[s, t, c] ), s = 0 .. S-1 in order
-__global__ __launch_bounds__(256) void gemv_reduce(const float* __restrict__ part, int S, int M, int64_t n_total,
-                                                   uint16_t* __restrict__ y, int64_t ldy) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * n_total) return;
-  int64_t t = i / n_total, c = i % n_total;
-  float a = 0.f;
-  for (int s = 0; s < S; ++s) a += part[(int64_t)s * M * n_total + i];
-  y[t * ldy + c] = __builtin_bit_cast(uint16_t, (__bf16)a);
+  const bool row_ok = lane < dsc[D_NVALID];
+  const int64_t col = (int64_t)dsc[D_COL0] + lane;
+  if (part == nullptr) {
+    if (row_ok)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 4 * g + i;
+          if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)acc[g][i]);
+        }
+    return;
+  }
+  // Partials are exchanged through device-coherent accesses only (agent-scope atomic stores and
+  // loads, which bypass the per-XCD L2's non-coherent lines), ordered by waiting for the stores'
+  // completion before the arrival count: no L2-wide writeback / invalidate fence is needed.
+  const int s = dsc[D_SPLIT];
+  if (row_ok)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * g + i;
+        if (t < M)
+          __hip_atomic_store(&part[((int64_t)s * M + t) * n_total + col], acc[g][i], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial stores are complete
+  int arrived = 0;
+  if (lane == 0) arrived = __hip_atomic_fetch_add(&ctr[dsc[D_CTR]], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  arrived = __shfl(arrived, 0);
+  if (arrived != split - 1) return;
+  if (row_ok)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 4 * g + i;
+        if (t < M) {
+          float a = 0.f;
+          for (int q = 0; q < split; ++q)
+            a += __hip_atomic_load(&part[((int64_t)q * M + t) * n_total + col], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)a);
+        }
+      }
+  if (lane == 0) __hip_atomic_store(&ctr[dsc[D_CTR]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
 template <int G>
-static void launch_g(int only, dim3 grid, hipStream_t st, const uint8_t* packed, const int32_t* desc, const uint16_t* x,
-                     int64_t ldx, int M, uint16_t* y, int64_t ldy, float* part, int64_t n_total) {
+static void launch_g(int only, dim3 grid, hipStream_t st, const uint8_t* packed, const int32_t* desc,
+                     const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, float* part, int* ctr,
+                     int64_t n_total, int split) {
+  const size_t lds = 0;
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, dim3(256), 0, st, packed, desc, x, ldx, M, y, ldy, part, n_total); return;
+#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, dim3(256), lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split); return;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, dim3(256), 0, st, packed, desc, x, ldx, M, y, ldy, part, n_total);
+      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, dim3(256), lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split);
   }
 }
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, void* y, int64_t ldy, float* partials, int split, int64_t n_total, hipStream_t st) {
+                int M, int G, void* y, int64_t ldy, float* partials, int* counters, int split, int64_t n_total,
+                hipStream_t st) {
   dim3 grid(n_desc);
   float* part = split > 1 ? partials : nullptr;
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   switch (G) {
-    case 1: launch_g<1>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, n_total); break;
-    case 2: launch_g<2>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, n_total); break;
-    case 4: launch_g<4>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, n_total); break;
-    case 8: launch_g<8>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, n_total); break;
+    case 1: launch_g<1>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 2: launch_g<2>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 4: launch_g<4>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 8: launch_g<8>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
     default: return GQK_ERR_FORM;
-  }
-  if (split > 1) {
-    int64_t total = (int64_t)M * n_total;
-    hipLaunchKernelGGL(gemv_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, partials, split, M, n_total,
-                       yy, ldy);
   }
   return GQK_OK;
 }

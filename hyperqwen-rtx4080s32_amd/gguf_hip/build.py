@@ -23,6 +23,8 @@ FLAGS = [
     "-I", os.path.join(REPO, "include"), "-I", CSRC,
     # packed fp32 VALU ops stay off (the pool's boxes have shown silent errors from them)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (no v_accvgpr_read round trips in the GEMV epilogue)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

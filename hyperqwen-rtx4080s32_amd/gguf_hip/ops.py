@@ -47,13 +47,14 @@ def type_info(weight_type: int) -> tuple[int, int, int, int]:
     return tuple(info)
 
 
-def type_planes(weight_type: int) -> list[tuple[int, int, int, int, int]]:
-    """The type's tile planes: (bytes per row, segments, first raw offset, segment bytes, stride)."""
+def type_planes(weight_type: int) -> list[tuple[int, int, int, int, int, int]]:
+    """The type's tile planes: (bytes per row, segments, first raw offset, segment bytes, stride,
+    column width)."""
     nplanes = type_info(weight_type)[3]
     info = (ctypes.c_int32 * 4)()
-    planes = (ctypes.c_int32 * (5 * nplanes))()
+    planes = (ctypes.c_int32 * (6 * nplanes))()
     check(lib.gqk_type_info(int(weight_type), info, planes), f"type_info({weight_type})")
-    return [tuple(planes[5 * p:5 * p + 5]) for p in range(nplanes)]
+    return [tuple(planes[6 * p:6 * p + 6]) for p in range(nplanes)]
 
 
 def quant_shape(weight_type: int, n: int, row_bytes: int) -> tuple[int, int]:
@@ -167,6 +168,9 @@ class GroupedLayer:
     K: int
     descs: list[torch.Tensor] = field(default_factory=list)
     plans: list[int] = field(default_factory=list)    # flattened GqkPlanInfo tuples, one per bucket
+    # split-K workspace of the GEMV plans: arrival counters (zeroed once here, left zero by every
+    # launch) and fp32 partials; calls on one layer must not overlap in time
+    workspace: torch.Tensor | None = None
 
     @property
     def n_total(self) -> int:
@@ -188,10 +192,13 @@ def prepare_grouped_layer(tiles_list: list[torch.Tensor], n_outs: list[int], wty
         shards.append((wt, n, off))
         off += t.numel()
     gl = GroupedLayer(packed, views, list(n_outs), list(wtypes), K)
+    ws = 0
     for m in GEMV_BUCKETS + GEMM_PLAN_M:
         info, desc = plan(shards, K, m, target_wgs)
         gl.descs.append(desc.to(packed.device))
         gl.plans.extend(info.as_tuple())
+        ws = max(ws, info.workspace_bytes)
+    gl.workspace = torch.zeros(max(ws, 256) // 4, dtype=torch.int32, device=packed.device)
     return gl
 
 
@@ -218,35 +225,31 @@ def _pick_plan(plans: list[int], M: int) -> int:
 
 
 def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
-                  n_total: int) -> torch.Tensor:
+                  n_total: int, workspace: torch.Tensor) -> torch.Tensor:
     M = int(x.shape[0])
     out = torch.empty((M, n_total), dtype=torch.bfloat16, device=x.device)
     if M == 0:
         return out
     i = _pick_plan(plans, M)
     info = GqkPlanInfo.from_tuple(plans[i * _NPLAN:(i + 1) * _NPLAN])
-    ws = None
-    ws_bytes = 0
-    if info.form == _lib.GQK_FORM_GEMV and info.split > 1:
-        ws_bytes = info.split * M * info.n_total * 4
-        ws = torch.empty(ws_bytes // 4, dtype=torch.float32, device=x.device)
     check(lib.gqk_linear(ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(descs[i].data_ptr()), ctypes.byref(info),
                          ctypes.c_void_p(x.data_ptr()), x.stride(0), M, ctypes.c_void_p(out.data_ptr()), out.stride(0),
-                         ctypes.c_void_p(ws.data_ptr() if ws is not None else 0), ws_bytes, _stream(x.device)),
+                         ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
+                         _stream(x.device)),
           "fused_mul_mat_gguf_grouped")
     return out
 
 
-@torch.library.custom_op("gguf_hip::fused_mul_mat_gguf_grouped", mutates_args=())
+@torch.library.custom_op("gguf_hip::fused_mul_mat_gguf_grouped", mutates_args=("workspace",))
 def fused_mul_mat_gguf_grouped(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
-                               n_total: int) -> torch.Tensor:
+                               n_total: int, workspace: torch.Tensor) -> torch.Tensor:
     """x bf16 [M, K] -> bf16 [M, n_total]: one launch over a grouped layer's shards (columns in
-    shard order)."""
-    return _grouped_impl(x, packed, descs, plans, n_total)
+    shard order).  workspace: the layer's split-K counters and partials."""
+    return _grouped_impl(x, packed, descs, plans, n_total, workspace)
 
 
 @fused_mul_mat_gguf_grouped.register_fake
-def _(x, packed, descs, plans, n_total):
+def _(x, packed, descs, plans, n_total, workspace):
     return torch.empty((x.shape[0], n_total), dtype=torch.bfloat16, device=x.device)
 
 
@@ -260,7 +263,7 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer) -> torch.Tensor:
     xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
     if xb.stride(1) != 1 or xb.stride(0) % 8 or xb.data_ptr() % 16:
         xb = xb.contiguous()
-    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total)
+    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace)
     return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
 
 

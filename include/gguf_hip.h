@@ -49,7 +49,7 @@ typedef struct gqk_plan_info {
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
   int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4, 8) */
   int32_t bm;         /* GEMM: tokens per workgroup (64, 128) */
-  int32_t split;      /* GEMV: split-K factor (partials + fixed-order reduce when > 1) */
+  int32_t split;      /* GEMV: split-K factor (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
   int32_t nb;         /* K / 256 */
@@ -64,8 +64,8 @@ const char* gqk_last_error(void);
 int gqk_version(void);
 
 /* Host-only metadata of a GGML type: info[0..3] = weights per block, bytes per block, bytes per
- * 256 weights, number of tile planes; planes (if not NULL, 5 ints per plane) = bytes per row,
- * segments, first raw offset, segment bytes, segment stride.  Replaces the reference's tile
+ * 256 weights, number of tile planes; planes (if not NULL, 6 ints per plane) = bytes per row,
+ * segments, first raw offset, segment bytes, segment stride, column width of the tile layout.  Replaces the reference's tile
  * registry TILE_TYPES (gguf-plugin/gluon/tiles.py:24-36) and gguf.GGML_QUANT_SIZES. */
 int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes);
 
@@ -97,9 +97,11 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
              int64_t desc_capacity, gqk_plan_info* info);
 
 /* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T over the grouped layer's shards (columns in shard
- * order), on `stream`.  desc_dev: the plan's descriptor table in device memory; workspace: at
- * least info->workspace_bytes of device memory when info->split > 1 (else may be NULL).  M must
- * be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
+ * order), on `stream`.  desc_dev: the plan's descriptor table in device memory.  workspace: when
+ * info->split > 1, at least info->workspace_bytes of 256-byte aligned device memory holding the
+ * split-K arrival counters (first) and fp32 partials; it must be zero-filled before its first
+ * use, every launch leaves the counters at zero again, and launches sharing one workspace must
+ * not overlap in time (else NULL).  M must be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,

@@ -35,8 +35,8 @@ def test_type_tables(wt):
     planes = ops.type_planes(wt)
     assert len(planes) == nplanes
     covered = []
-    for size, nseg, off, seglen, stride in planes:
-        assert size == nseg * seglen
+    for size, nseg, off, seglen, stride, width in planes:
+        assert size == nseg * seglen and size % width == 0 and width in (2, 4, 8, 16)
         for s in range(nseg):
             covered += list(range(off + s * stride, off + s * stride + seglen))
     assert sorted(covered) == list(range(rec))          # every raw byte of the record exactly once
@@ -79,13 +79,14 @@ def test_plan_gemv_balanced_split_partition():
         d = _rows(desc)
         S = info.split
         assert info.form == 1 and info.g == 1 and info.m_max == 4
-        assert d.shape[0] == info.n_desc == 24 * S
-        first = d[d[:, 3] == 0]                          # the workgroup of tiles 0..3
+        assert d.shape[0] == info.n_desc == 96 * S        # one workgroup per (64-row tile, split)
+        first = d[d[:, 3] == 0]                          # the workgroups of tile 0
         assert first[:, 5].tolist() == [s * 20 // S for s in range(S)]
         assert first[:, 6].tolist() == [(s + 1) * 20 // S for s in range(S)]
-        assert first[:, 7].tolist() == list(range(S))
-        assert (first[:, 6] > first[:, 5]).all() and 1 <= S <= 10
-        assert info.workspace_bytes == (S * 4 * 6144 * 4 if S > 1 else 0)
+        assert first[:, 7].tolist() == list(range(S)) and (first[:, 11] == 0).all()
+        assert (first[:, 6] > first[:, 5]).all() and 1 <= S <= 5
+        assert sorted(set(d[:, 11].tolist())) == list(range(96))   # one arrival counter per tile
+        assert info.workspace_bytes == (512 + S * 4 * 6144 * 4 if S > 1 else 0)
 
 
 def test_plan_descriptor_rows_mixed_layer():
@@ -96,12 +97,12 @@ def test_plan_descriptor_rows_mixed_layer():
     info, desc = ops.plan([(21, 70, 0), (12, 300, off2)], K, 8, 4)
     d = _rows(desc)
     assert info.types_mask == 0 and info.n_total == 370 and info.g == 2
-    assert info.split == 1
-    # IQ3_S: 2 tiles in one workgroup; Q4_K: 5 tiles in two (4 + 1)
-    assert d[:, 0].tolist() == [21, 12, 12]
-    assert d[:, 3].tolist() == [0, 0, 4] and d[:, 4].tolist() == [2, 4, 1]
-    assert d[:, 8].tolist() == [0, 70, 70 + 256] and d[:, 9].tolist() == [70, 256, 44]
-    assert d[1, 1] == off2 and d[:, 10].tolist() == [3, 3, 3]
+    assert info.split == 1 and info.workspace_bytes == 0
+    # one workgroup per tile: IQ3_S 2 tiles (64 + 6 rows), Q4_K 5 tiles (4 x 64 + 44)
+    assert d[:, 0].tolist() == [21, 21, 12, 12, 12, 12, 12]
+    assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
+    assert d[:, 8].tolist() == [0, 64, 70, 134, 198, 262, 326] and d[:, 9].tolist() == [64, 6, 64, 64, 64, 64, 44]
+    assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 11].tolist() == list(range(7))
     gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 2048)
     g = _rows(gd)
     assert gi.form == 2 and gi.bm == 128 and g.shape[0] == 1 + 3

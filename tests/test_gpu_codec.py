@@ -66,9 +66,10 @@ def _np_repack(raw, wt, n, K, planes, rec):
     rows[:n] = raw.reshape(n, nb, rec)
     out = np.zeros((ntiles, nb, 64 * rec), np.uint8)
     poff = 0
-    for size, nseg, off, seglen, stride in planes:
+    for size, nseg, off, seglen, stride, width in planes:
         idx = np.concatenate([np.arange(off + s * stride, off + s * stride + seglen) for s in range(nseg)])
-        block = rows[:, :, idx].reshape(ntiles, 64, nb, size).transpose(0, 2, 1, 3).reshape(ntiles, nb, 64 * size)
+        block = rows[:, :, idx].reshape(ntiles, 64, nb, size // width, width)   # tile, row, kb, column, byte
+        block = block.transpose(0, 2, 3, 1, 4).reshape(ntiles, nb, 64 * size)    # column-major: column, row, byte
         out[:, :, 64 * poff:64 * (poff + size)] = block
         poff += size
     return out.reshape(-1)

@@ -66,6 +66,28 @@ def test_gemv_split_k_ragged(dev, wt):
             assert e < TOL, (G.NAMES[wt], target, M, e)
 
 
+def test_split_k_repeat_is_bit_identical(dev):
+    """The in-kernel split-K exchange (partials, arrival counters) under repetition: every
+    launch of one plan gives the same bits, and the counters return to zero."""
+    import gguf_hip
+
+    rng = np.random.default_rng(11)
+    n, K = 1000, 40 * 256
+    raw = G.random_blocks(rng, n, K, G.Q4_K)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K], target_wgs=4096)
+    plan = gl.plans[:10]
+    assert plan[4] > 1, "the plan must split K"
+    wf = G.dequantize(raw, G.Q4_K)
+    for M in (1, 8):
+        x = _x(M, K, 7000 + M, dev)
+        y0 = gguf_hip.mul_mat_grouped(x, gl)
+        assert G.rel_err(y0.float().cpu().numpy(), _ref(x, wf)) < TOL
+        for _ in range(30):
+            assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y0)
+    torch.cuda.synchronize()
+    assert int(gl.workspace[:((n + 63) // 64)].abs().sum()) == 0
+
+
 def test_mixed_layer_one_launch(dev):
     """A merged layer of three types in one grouped launch; with split 1 every shard's columns
     are bit-identical to its own launch (the reference's mixed-layer identity,
