@@ -61,44 +61,72 @@ def _capture(fn, torch):
     return g
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict:
-    """The reference CPU path on a bounded sample: oracle dequant (numpy, one thread) + fp32
-    torch.matmul (torch's threads) of row samples of the Q4_K and Q6_K gate_up shards, M = 8."""
+def _traffic(symbol: str, dom: dict, M: int):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading on a plain copy of
+    known size), or None when no summary matches this kernel and workload."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path, encoding="utf-8") as f:
+        rec = json.load(f)
+    for r in rec.get("kernels", []):
+        if r.get("symbol") == symbol and r.get("N") == dom["N"] and r.get("K") == dom["K"] and r.get("M") == M:
+            return r["hbm_bytes_per_launch"]
+    return None
+
+
+def cpu_baseline(seconds: float = 15.0) -> dict:
+    """The reference CPU path on a bounded sample: oracle dequant (numpy, row chunks on a thread
+    pool) + fp32 torch.matmul over the whole Q4_K and Q6_K gate_up shards at M = 8, passes
+    repeated for about `seconds` (at least 3), median pass reported."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
     import torch
 
     from oracle import ggml_ref as G
 
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    pool = ThreadPoolExecutor(cores)
     rng = np.random.default_rng(0)
     K, M = 5120, 8
     x = torch.randn(M, K)
 
-    def one(rows):
+    def deq(raw, wt):
+        chunks = np.array_split(raw, cores)
+        return np.concatenate(list(pool.map(lambda c: G.dequantize(c, wt), chunks)))
+
+    rows = 34816                                              # the whole gate_up shard of each type
+    raws = {wt: G.random_blocks(rng, rows, K, wt) for wt in (Q4_K, Q6_K)}
+    nbytes = sum(r.nbytes for r in raws.values())
+
+    def one():
         t_deq = t_mm = 0.0
-        nbytes = 0
-        for wt in (Q4_K, Q6_K):
-            raw = G.random_blocks(rng, rows, K, wt)
+        for wt, raw in raws.items():
             t0 = time.perf_counter()
-            w = torch.from_numpy(G.dequantize(raw, wt))
+            w = torch.from_numpy(deq(raw, wt))
             t1 = time.perf_counter()
             y = x @ w.T
             t2 = time.perf_counter()
             assert y.shape == (M, rows)
             t_deq += t1 - t0
             t_mm += t2 - t1
-            nbytes += raw.nbytes
-        return t_deq, t_mm, nbytes
+        return t_deq, t_mm
 
-    d, m, b = one(256)                                       # calibrate
-    rows = int(max(256, min(34816, 256 * (seconds / 3) / max(d + m, 1e-3))))
-    runs = [one(rows) for _ in range(3)]
+    runs = []
+    t_start = time.perf_counter()
+    while len(runs) < 3 or (time.perf_counter() - t_start < seconds and len(runs) < 50):
+        runs.append(one())
     td = statistics.median(r[0] for r in runs)
     tm = statistics.median(r[1] for r in runs)
-    nbytes = runs[0][2]
-    return {"value": round(nbytes / (td + tm) / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+    pool.shutdown()
+    return {"value": round(nbytes / (td + tm) / 1e9, 4), "unit": "GB/s", "cores": cores,
             "kind": "port",
-            "sample": f"Q4_K+Q6_K gate_up rows 0..{rows} of 34816 x K=5120, M={M}: oracle dequant "
-                      f"{td * 1e3:.1f} ms (1 thread) + torch fp32 matmul {tm * 1e3:.1f} ms, median of 3",
+            "sample": f"whole Q4_K + Q6_K gate_up shards (34816 x 5120 each, {nbytes} packed bytes), M={M}: "
+                      f"oracle dequant {td * 1e3:.1f} ms + torch fp32 matmul {tm * 1e3:.1f} ms per pass on "
+                      f"{cores} threads, median of {len(runs)} passes",
             "dequant_ms": round(td * 1e3, 2), "matmul_ms": round(tm * 1e3, 2)}
 
 
@@ -112,6 +140,11 @@ def main() -> int:
     ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--detail", action="store_true", help="print the per-shard table to stderr")
+    ap.add_argument("--only", default="", help="TYPE:SHARD (e.g. Q6_K:gate_up): run that shard alone, "
+                    "so a profiler's per-kernel statistics cover exactly one launch shape")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB 3 times (the byte-counter calibration "
+                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the GGUF linear path has no collective; "
@@ -125,10 +158,20 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calib_copy:
+        src = torch.ones(args.calib_copy << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     M = args.m
     shards = []                     # (type, name, N, K, [GroupedLayer per copy], bytes)
+    only = tuple(args.only.split(":")) if args.only else None
     for wt in (Q4_K, Q6_K):
         for name, N, K in SHAPES:
+            if only and (gguf_hip.TYPE_NAMES[wt], name) != only:
+                continue
             gls = []
             for c in range(args.copies):
                 W = random_shard(N, K, wt, dev, seed=1000 * c + N + wt)
@@ -166,18 +209,24 @@ def main() -> int:
     rows = []
     for wt, name, N, K, gls, nb in shards:
         def f(gls=gls, K=K):
-            for gl in gls:
-                gguf_hip.mul_mat_grouped(xs[K], gl)
+            for _ in range(4):
+                for gl in gls:
+                    gguf_hip.mul_mat_grouped(xs[K], gl)
         g = _capture(f, torch)
         g.replay()
-        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / len(gls)
+        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (4 * len(gls))
         plan = gls[0].plans[[4, 8, 16, 32].index(next(b for b in (4, 8, 16, 32) if M <= b)) * 10:][:10]
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
-                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "split": plan[4], "wgs": plan[5]})
+                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": plan[2], "split": plan[4], "wgs": plan[5]})
         del g
     dom = max(rows, key=lambda r: r["us"])
-    dom_bytes = next(s[5] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
+    dom_wt = next(s[0] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
+    dom_w = next(s[5] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
+    # algorithmic bytes of one launch: packed weights + x (bf16) read once + y (bf16) written once
+    dom_bytes = dom_w + 2 * M * dom["K"] + 2 * M * dom["N"]
     achieved = dom_bytes / (dom["us"] * 1e-6) / 1e9
+    dom_symbol = f"gqk::gemv_kernel<{dom['g']}, {dom_wt}>"
+    traffic = _traffic(dom_symbol, dom, M)
     if args.detail:
         for r in rows:
             print(json.dumps(r), file=sys.stderr)
@@ -186,7 +235,7 @@ def main() -> int:
     if args.gemm_m:
         del graphs
         Mg = args.gemm_m
-        wt, name, N, K, gls, nb = next(s for s in shards if s[0] == Q4_K and s[1] == "gate_up")
+        wt, name, N, K, gls, nb = next((s for s in shards if s[0] == Q4_K and s[1] == "gate_up"), shards[0])
         xg = torch.randn(Mg, K, device=dev).to(torch.bfloat16)
 
         def fg():
@@ -196,7 +245,7 @@ def main() -> int:
         g.replay()
         t = statistics.median(_time_graph(g, 3, torch) for _ in range(3)) / len(gls)
         tflops = 2.0 * Mg * N * K / (t * 1e-3) / 1e12
-        gemm = {"type": "Q4_K", "shard": "gate_up", "N": N, "K": K, "M": Mg, "ms": round(t, 4),
+        gemm = {"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "M": Mg, "ms": round(t, 4),
                 "TFLOPs": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
     out = {
@@ -208,8 +257,8 @@ def main() -> int:
                    "M": M, "copies": args.copies, "bytes_per_step": step_bytes,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": f"{dom['type']} {dom['shard']} {dom['N']}x{dom['K']} M={M}",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": f"{dom['type']} {dom['shard']} {dom['N']}x{dom['K']} M={M}", "symbol": dom_symbol,
                      "launch_us": dom["us"], "bytes_per_launch": dom_bytes},
         "shards": rows,
         "gemm": gemm,

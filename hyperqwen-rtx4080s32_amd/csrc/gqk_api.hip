@@ -30,12 +30,15 @@ int check_launch(const char* what) {
   return GQK_OK;
 }
 
-// GEMV workgroup target when the caller gives none: about four 4-wave workgroups per CU of a
-// 256-CU MI355X, so every SIMD holds four waves streaming weights.
-constexpr int kDefaultTargetWgs = 1024;
+// GEMV workgroup target when the caller gives none: two 4-wave workgroups per CU of a 256-CU
+// MI355X.  Small shards split K to reach it; large ones (>= 512 tiles) run one workgroup per
+// tile, all resident at once (a second generation of workgroups costs more than it hides).
+constexpr int kDefaultTargetWgs = 512;
 
 // bytes of the split-K arrival counters of `tiles` tiles (rounded to 256 so the partials stay aligned)
 int64_t gqk_counter_bytes(int64_t tiles) { return (tiles * 4 + 255) / 256 * 256; }
+// bytes of the fp32 split-K partials: [tile][split][64 rows][m_max tokens]
+int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return tiles * split * 64 * m_max * 4; }
 
 }  // namespace
 
@@ -164,6 +167,9 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   if (M <= 32) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
+#ifdef GQK_GEMV_MIN_G
+    pi.g = std::max(pi.g, GQK_GEMV_MIN_G);
+#endif
     pi.m_max = 4 * pi.g;
     // one workgroup per (tile, k-range), its four waves taking quarters of the k-range: enough
     // workgroups to fill the chip, each wave keeping >= 2 super-blocks where the shape allows
@@ -171,7 +177,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     int64_t split = (target + tiles - 1) / tiles;
     int64_t cap = std::max<int64_t>(1, nb / 8);
     if (tiles * cap < 512) cap = std::max<int64_t>(1, nb / 4);
-    split = std::max<int64_t>(1, std::min(split, cap));
+    split = std::max<int64_t>(1, std::min({split, cap, (int64_t)GQK_SPLIT_MAX}));
     pi.split = (int32_t)split;
     int64_t col0 = 0, ctr = 0;
     for (int i = 0; i < nshards; ++i) {
@@ -182,8 +188,8 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
       col0 += shards[i].n;
     }
     // workspace: tile arrival counters (zero before the first launch, left zero by each launch),
-    // then the fp32 partials [split][M][n_total]
-    pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + (int64_t)split * pi.m_max * n_total * 4 : 0;
+    // then the fp32 partials [tile][split][64 rows][m_max tokens]
+    pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
     pi.bm = M <= 64 ? 64 : 128;
@@ -229,7 +235,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     if (info->split > 1) {
       tiles = info->n_desc / info->split;   // one descriptor row per (tile, split)
       const int64_t cb = gqk_counter_bytes(tiles);
-      const int64_t need = cb + (int64_t)info->split * M * info->n_total * 4;
+      const int64_t need = cb + gqk_partial_bytes(tiles, info->split, 4 * info->g);
       if (!workspace || workspace_bytes < need)
         return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);
       if ((uintptr_t)workspace & 255) return fail(GQK_ERR_SHAPE, "linear: workspace not 256-byte aligned");

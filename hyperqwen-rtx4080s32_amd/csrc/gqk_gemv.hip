@@ -24,7 +24,7 @@
 // fp32 matmul of the gguf-py weights up to summation order.
 //
 // Split-K: with more than one k-range per tile the workgroups write fp32 partials
-// [split][M][n_total]; the last workgroup of a tile to arrive sums them in split order
+// [tile][split][row][token]; the last workgroup of a tile to arrive sums them in split order
 // (deterministic, one rounding to bf16), the reference's sum_partials
 // (gguf-plugin/gluon/tiles_grouped.py:142-162) fused into the same launch.
 #include <hip/hip_runtime.h>
@@ -34,6 +34,9 @@
 namespace gqk {
 
 typedef short v4s __attribute__((ext_vector_type(4)));
+// buffer resource word 3 (raw untyped dword access) and the device-scope cache policy (sc1)
+#define GQK_BUF_WORD3 0x00020000
+#define GQK_CPOL_SC1 16
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 
@@ -378,6 +381,17 @@ __device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const 
   }
 }
 
+// Records held per wave: two (one decoded while the next is in flight).  A third costs a wave
+// per SIMD of occupancy, and measured slower for every format: more waves hide more latency.
+template <int G, int T>
+__host__ __device__ constexpr int gemv_depth() {
+#ifdef GQK_GEMV_DEPTH
+  return GQK_GEMV_DEPTH;
+#else
+  return 2;
+#endif
+}
+
 // One wave: weight rows of tile `tile`, super-blocks [kw0, kw1), accumulating into acc.
 template <int G, int T>
 __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
@@ -426,24 +440,40 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
     }
   };
 
-  // Straight-line pipeline per super-block: the next super-block's x loads and record loads are
-  // issued before this one is decoded; its x is written to LDS after (waiting for the x loads
-  // only, which precede the record loads), and the record hand-off is the only wait on those.
-  uint4 xv[NI][4];
-  stage_load<MPAD>(x, ldx, M, kw0, lane, xv);
-  D cur;
-  cur.load(tbase + (int64_t)kw0 * 64 * D::REC, lane);
-  stage_store<MPAD, D::FAM>(wl, M, lane, xv);
-  for (int kb = kw0; kb < kw1; ++kb) {
-    D nxt;
-    const bool more = kb + 1 < kw1;
-    if (more) {
-      stage_load<MPAD>(x, ldx, M, kb + 1, lane, xv);
-      nxt.load(tbase + (int64_t)(kb + 1) * 64 * D::REC, lane);
+  // Register pipeline DEPTH super-blocks deep: while record kb is decoded, the records (and the
+  // x slices) of kb+1 .. kb+DEPTH-1 are in flight.  Each step issues x(kb+DEPTH) and then the
+  // record kb+DEPTH, so every wait (x of a step before its LDS write, the record before its
+  // decode) covers exactly the loads it needs under the in-order vmcnt count.  Every load is
+  // unconditional (addresses clamped to the wave's last super-block, so the tail re-reads it
+  // from L2) and the buffers rotate by code position, never by copy.
+  constexpr int DEPTH = gemv_depth<G, T>();
+  const int last = kw1 - 1;
+  auto rec = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
+  uint4 x0[NI][4], x1[NI][4], x2[NI][4];
+  D r0, r1, r2;
+  stage_load<MPAD>(x, ldx, M, kw0, lane, x0);
+  r0.load(rec(kw0), lane);
+  stage_load<MPAD>(x, ldx, M, min(kw0 + 1, last), lane, x1);
+  r1.load(rec(kw0 + 1), lane);
+  if constexpr (DEPTH == 3) {
+    stage_load<MPAD>(x, ldx, M, min(kw0 + 2, last), lane, x2);
+    r2.load(rec(kw0 + 2), lane);
+  }
+  auto step = [&](D& r, uint4 (&xv)[NI][4], int kb) {
+    stage_store<MPAD, D::FAM>(wl, M, lane, xv);
+    process(r);
+    stage_load<MPAD>(x, ldx, M, min(kb + DEPTH, last), lane, xv);
+    r.load(rec(kb + DEPTH), lane);
+  };
+  for (int kb = kw0;; kb += DEPTH) {
+    step(r0, x0, kb);
+    if (kb + 1 > last) break;
+    step(r1, x1, kb + 1);
+    if constexpr (DEPTH == 3) {
+      if (kb + 2 > last) break;
+      step(r2, x2, kb + 2);
     }
-    process(cur);
-    if (more) stage_store<MPAD, D::FAM>(wl, M, lane, xv);
-    cur = nxt;
+    if (kb + DEPTH > last) break;
   }
 }
 
@@ -479,8 +509,19 @@ __host__ __device__ constexpr int gemv_lds_bytes(bool tables) {
 // waves' sums combined through LDS in a fixed order; with split-K (part != nullptr) the fp32
 // partial goes to part[split] and the last workgroup of the tile to arrive (counter ctr[tile])
 // sums the partials in split order and writes y, then resets the counter.
+// Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 fits
+// three waves without spilling and runs faster there than at the allocator's own choice of two.
 template <int G, int ONLY>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
+constexpr int gemv_waves() {
+#ifdef GQK_GEMV_WAVES
+  return GQK_GEMV_WAVES;
+#else
+  return (G == 2 && ONLY == GQK_Q6_K) ? 3 : 1;
+#endif
+}
+
+template <int G, int ONLY>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>()))) void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
                                                    const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                    uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
                                                    int* __restrict__ ctr, int64_t n_total, int split) {
@@ -539,39 +580,51 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ p
         }
     return;
   }
-  // Partials are exchanged through device-coherent accesses only (agent-scope atomic stores and
-  // loads, which bypass the per-XCD L2's non-coherent lines), ordered by waiting for the stores'
-  // completion before the arrival count: no L2-wide writeback / invalidate fence is needed.
+  // Split-K exchange.  The partials of a tile sit at part[tile][split][lane][MPAD] (1 KiB x G per
+  // workgroup, written as 16-byte stores).  They move through device-coherent (sc1) buffer
+  // accesses only, which write through / bypass the per-XCD L2's non-coherent lines, and the
+  // stores complete before the arrival count: no L2-wide writeback or invalidate is needed.
   const int s = dsc[D_SPLIT];
-  if (row_ok)
+  const int ctr_i = dsc[D_CTR];
+  float* tp = part + (int64_t)ctr_i * split * 64 * MPAD;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, split * 64 * MPAD * 4, GQK_BUF_WORD3);
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 4 * g + i;
-        if (t < M)
-          __hip_atomic_store(&part[((int64_t)s * M + t) * n_total + col], acc[g][i], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-      }
+  for (int g = 0; g < G; ++g)
+    __builtin_amdgcn_raw_buffer_store_b128(acc[g], rs, ((s * 64 + lane) * MPAD + 4 * g) * 4, 0, GQK_CPOL_SC1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial stores are complete
   int arrived = 0;
-  if (lane == 0) arrived = __hip_atomic_fetch_add(&ctr[dsc[D_CTR]], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) arrived = __hip_atomic_fetch_add(&ctr[ctr_i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   arrived = __shfl(arrived, 0);
   if (arrived != split - 1) return;
+  asm volatile("" ::: "memory");
+  // the last workgroup: every partial of the tile, QC splits per round trip, summed in split order
+  constexpr int QC = G <= 2 ? 8 : (G == 4 ? 4 : 2);
+  v4f a[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) a[g] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int q0 = 0; q0 < split; q0 += QC) {
+    v4f v[QC][G];
+#pragma unroll
+    for (int j = 0; j < QC; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        v[j][g] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((min(q0 + j, split - 1) * 64 + lane) * MPAD + 4 * g) * 4,
+                                                        0, GQK_CPOL_SC1);
+#pragma unroll
+    for (int j = 0; j < QC; ++j)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (q0 + j < split) a[g] += v[j][g];
+  }
   if (row_ok)
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 4 * g + i;
-        if (t < M) {
-          float a = 0.f;
-          for (int q = 0; q < split; ++q)
-            a += __hip_atomic_load(&part[((int64_t)q * M + t) * n_total + col], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)a);
-        }
+        if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)a[g][i]);
       }
-  if (lane == 0) __hip_atomic_store(&ctr[dsc[D_CTR]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+  if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
 template <int G>

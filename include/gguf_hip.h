@@ -54,7 +54,7 @@ typedef struct gqk_plan_info {
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
   int32_t nb;         /* K / 256 */
   int64_t n_total;    /* output columns: sum of the shards' rows */
-  int64_t workspace_bytes; /* device workspace gqk_linear needs at M = m_max */
+  int64_t workspace_bytes; /* device workspace gqk_linear needs (any M <= m_max) */
 } gqk_plan_info;
 
 /* Last error message of the calling thread ("" when none). */
