@@ -192,13 +192,15 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
-    pi.bm = M <= 64 ? 64 : 128;
+    // 64 / 128 tokens x 128 rows per workgroup up to 128 tokens; 256 x 256 above
+    pi.bm = M <= 64 ? 64 : M <= 128 ? 128 : 256;
     pi.m_max = 1 << 30;
     pi.split = 1;
+    const int64_t per = pi.bm == 256 ? 4 : 2;   // tiles per descriptor row
     int64_t col0 = 0;
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
-      for (int64_t t0 = 0; t0 < ntile; t0 += 2) row(i, t0, (int)std::min<int64_t>(2, ntile - t0), 0, nb, 0, col0, 0);
+      for (int64_t t0 = 0; t0 < ntile; t0 += per) row(i, t0, (int)std::min<int64_t>(per, ntile - t0), 0, nb, 0, col0, 0);
       col0 += shards[i].n;
     }
     pi.workspace_bytes = 0;
@@ -212,6 +214,18 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     memcpy(desc, rows.data(), rows.size() * sizeof(int32_t));
   }
   return GQK_OK;
+}
+
+int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
+  if (!info) return fail(GQK_ERR_ARG, "linear_workspace_bytes: info is NULL");
+  if (M <= 0) return 0;
+  if (info->form == GQK_FORM_GEMV) return info->split > 1 ? info->workspace_bytes : 0;
+  if (info->form == GQK_FORM_GEMM) {
+    if (info->bm != 256) return 0;
+    const int64_t n = gqk::gemm_big_workspace(info->n_desc, M, info->nb);
+    return n < 0 ? fail(GQK_ERR_HIP, "linear_workspace_bytes: no HIP device") : n;
+  }
+  return fail(GQK_ERR_FORM, "linear_workspace_bytes: unknown form %d", info->form);
 }
 
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
@@ -251,7 +265,10 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     if (M <= 32) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
     if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
     int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
-                              info->bm, (hipStream_t)stream);
+                              info->bm, workspace, workspace_bytes, (hipStream_t)stream);
+    if (rc == GQK_ERR_SHAPE)
+      return fail(rc, "linear: GEMM workspace %lld bytes < %lld (or not 256-byte aligned)", (long long)workspace_bytes,
+                  (long long)gqk::gemm_big_workspace(info->n_desc, M, info->nb));
     if (rc) return fail(rc, "linear: GEMM launch form bm=%d", info->bm);
     return check_launch("linear (GEMM)");
   }

@@ -8,6 +8,7 @@
 // fp32 gguf-py value), stages the activations beside them, and runs v_mfma_f32_32x32x16_bf16
 // with fp32 accumulation.  Global loads of step s+1 are in flight while step s multiplies.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include "gqk_common.h"
 #include "gqk_internal.h"
 
@@ -15,6 +16,7 @@ namespace gqk {
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float g_h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFF));
@@ -439,6 +441,610 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ p
 #undef RUN
 }
 
+// ---- the 256 x 256 form (M > 128) ------------------------------------------------------------
+// Workgroup = 512 threads (8 waves, two per SIMD): 256 tokens x 256 weight rows (four tiles of one
+// shard), K in steps of 64.  Wave (wm, wn) owns tokens 64 wm .. +63 and rows 128 wn .. +127 (2 x 4
+// blocks of v_mfma_f32_32x32x16_bf16).  Per step each thread decodes 32 weights of one row (two
+// runs of 16 at step-local offsets OFF0 / OFF1, per type) and stages 32 activations of one token;
+// the next step's loads are in flight during the MFMAs.  LDS: x and weights double-buffered
+// (147,456 bytes) plus the IQ3_S tables, one workgroup per CU.
+
+#define GB_M 256
+#define GB_N 256
+#define GQK_GB_WORD3 0x00020000   // buffer resource word 3: raw untyped dword access
+#define GQK_GB_SC1 16             // device-scope cache policy (write through / bypass the XCD L2)
+#define GB_K 64
+#define GB_LD 72   // LDS row stride in bf16: 144 bytes, so 16 consecutive rows hit 16 distinct bank groups
+
+struct GTabs {
+  uint32_t kv[4];          // IQ4 kvalues + 128, four per dword
+  const uint32_t* grid;    // IQ3_S grid magnitudes (LDS, 512 words)
+  const uint4* sign;       // IQ3_S sign masks of a sign byte: bits 15 / 31 of four bf16 pairs (LDS)
+};
+
+// fma(dl, u_i, bias) for the four unsigned bytes u_i of u -> two bf16 pairs (RNE)
+__device__ __forceinline__ void cvt4(uint32_t u, float dl, float bias, uint32_t* o) {
+  o[0] = g_bf16x2(__builtin_fmaf(dl, (float)(u & 0xFF), bias), __builtin_fmaf(dl, (float)((u >> 8) & 0xFF), bias));
+  o[1] = g_bf16x2(__builtin_fmaf(dl, (float)((u >> 16) & 0xFF), bias), __builtin_fmaf(dl, (float)(u >> 24), bias));
+}
+// IQ4 lookup of four nibbles (bytes 0..15 of n): kvalues + 128 as four unsigned bytes
+__device__ __forceinline__ uint32_t kv4(uint32_t n, const GTabs& tb) {
+  const uint32_t s = n & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(tb.kv[1], tb.kv[0], s);
+  const uint32_t hi = __builtin_amdgcn_perm(tb.kv[3], tb.kv[2], s);
+  const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
+  return (hi & m) | (lo & ~m);
+}
+// Q4_K / Q5_K 6-bit scale and min of sub-block j (get_scale_min_k4) from the 12 scale bytes
+__device__ __forceinline__ void k4_scale(const uint32_t* hdr, int j, int& sc, int& m) {
+  const uint64_t s01 = (uint64_t)hdr[1] | ((uint64_t)hdr[2] << 32);
+  if (j < 4) {
+    sc = (int)((s01 >> (8 * j)) & 63);
+    m = (int)((s01 >> (8 * j + 32)) & 63);
+  } else {
+    const uint32_t b = (hdr[3] >> (8 * (j - 4))) & 0xFF;   // byte j + 4
+    sc = (int)((b & 0xF) | (((s01 >> (8 * (j - 4))) & 0xC0) >> 2));
+    m = (int)((b >> 4) | (((s01 >> (8 * j)) & 0xC0) >> 2));
+  }
+}
+// Q3_K signed 6-bit scale i (0..15) from the 12 packed bytes
+__device__ __forceinline__ int q3_scale(const uint32_t* sb, int i) {
+  const uint64_t s01 = (uint64_t)sb[0] | ((uint64_t)sb[1] << 32);
+  const int lo = (int)(((s01 >> (8 * (i & 7))) >> (4 * (i >> 3))) & 0xF);
+  const int hi = (int)((sb[2] >> (8 * (i & 3) + 2 * (i >> 2))) & 3);
+  return (lo | (hi << 4)) - 32;
+}
+
+template <int T> struct B2;
+
+template <> struct B2<GQK_Q4_0> {   // block b = 2 kq + h: low nibbles -> 16 weights, high -> next 16
+  uint32_t q[4], d;
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * kq + h)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * (2 * kq + h));
+  }
+  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float dd = g_h2f(d);
+    {
+      cvt4(q[i] & 0x0F0F0F0Fu, dd, -8.f * dd, o + 2 * i);
+      cvt4((q[i] >> 4) & 0x0F0F0F0Fu, dd, -8.f * dd, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_IQ4_NL> {
+  uint32_t q[4], d;
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * kq + h)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * (2 * kq + h));
+  }
+  __device__ void out(int, int, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    const float dd = g_h2f(d);
+    {
+      cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), dd, -128.f * dd, o + 2 * i);
+      cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), dd, -128.f * dd, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q5_0> {
+  uint32_t q[4], qh, d;
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    const int b = 2 * kq + h;
+    gld<16>(q, col16(c, r, b)); gld<4>(&qh, col16(c + 64 * 128, r, b >> 2) + 4 * (b & 3));
+    gld<2>(&d, c + 64 * 160 + r * 16 + 2 * b);
+  }
+  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float dd = g_h2f(d);
+    {
+      const uint32_t hl = ((((qh >> (4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+      const uint32_t hh = ((((qh >> (16 + 4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+      cvt4((q[i] & 0x0F0F0F0Fu) | hl, dd, -16.f * dd, o + 2 * i);
+      cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | hh, dd, -16.f * dd, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q8_0> {   // block b = 2 kq + h, 32 int8 in two 16-byte columns
+  uint32_t q[8], d;
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    const int b = 2 * kq + h;
+    gld<16>(q, col16(c, r, 2 * b)); gld<16>(q + 4, col16(c, r, 2 * b + 1)); gld<2>(&d, c + 64 * 256 + r * 16 + 2 * b);
+  }
+  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float dd = g_h2f(d);
+    cvt4(q[2 * i] ^ 0x80808080u, dd, -128.f * dd, o + 4 * i);
+    cvt4(q[2 * i + 1] ^ 0x80808080u, dd, -128.f * dd, o + 4 * i + 2);
+  }
+};
+
+template <> struct B2<GQK_Q2_K> {   // groups 2 kq, 2 kq + 1 share the 16 bytes of the row's part h
+  uint32_t q[4], scw, dd;
+  static __device__ int off0(int h) { return 16 * h; }
+  static __device__ int off1(int h) { return 32 + 16 * h; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * (kq >> 1) + h)); gld<4>(&scw, c + 64 * 64 + r * 16 + 4 * kq); gld<4>(&dd, c + 64 * 80 + r * 4);
+  }
+  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float d = g_h2f(dd), dmin = g_h2f(dd >> 16);
+    const uint32_t s0 = (scw >> (8 * h)) & 0xFF, s1 = (scw >> (8 * (2 + h))) & 0xFF;
+    const float dl0 = d * (float)(s0 & 0xF), b0 = -(dmin * (float)(s0 >> 4));
+    const float dl1 = d * (float)(s1 & 0xF), b1 = -(dmin * (float)(s1 >> 4));
+    const int j0 = 2 * (kq & 1);
+    {
+      cvt4((q[i] >> (2 * j0)) & 0x03030303u, dl0, b0, o + 2 * i);
+      cvt4((q[i] >> (2 * j0 + 2)) & 0x03030303u, dl1, b1, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q3_K> {
+  uint32_t q[4], hm[4], sb[3], d;
+  static __device__ int off0(int h) { return 16 * h; }
+  static __device__ int off1(int h) { return 32 + 16 * h; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * (kq >> 1) + h));
+    gld<16>(hm, col16(c + 64 * 64, r, h));
+    const uint32_t* p = (const uint32_t*)(c + 64 * 96);   // three 4-byte columns
+    sb[0] = p[r]; sb[1] = p[64 + r]; sb[2] = p[128 + r];
+    gld<2>(&d, c + 64 * 108 + r * 2);
+  }
+  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float dd = g_h2f(d);
+    const float dl0 = dd * (float)q3_scale(sb, 4 * kq + h), dl1 = dd * (float)q3_scale(sb, 4 * kq + 2 + h);
+    const int j0 = 2 * (kq & 1), g0 = 2 * kq;
+    {
+      const uint32_t u0 = ((q[i] >> (2 * j0)) & 0x03030303u) | (((hm[i] >> g0) & 0x01010101u) << 2);
+      const uint32_t u1 = ((q[i] >> (2 * j0 + 2)) & 0x03030303u) | (((hm[i] >> (g0 + 1)) & 0x01010101u) << 2);
+      cvt4(u0, dl0, -4.f * dl0, o + 2 * i);
+      cvt4(u1, dl1, -4.f * dl1, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q4_K> {   // low nibbles: sub-block 2 kq, high: 2 kq + 1; part h = bytes 16h .. 16h + 15
+  uint32_t q[4], hdr[4];
+  static __device__ int off0(int h) { return 16 * h; }
+  static __device__ int off1(int h) { return 32 + 16 * h; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * kq + h)); gld<16>(hdr, c + 64 * 128 + r * 16);
+  }
+  __device__ void out(int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    int sc0, m0, sc1, m1;
+    k4_scale(hdr, 2 * kq, sc0, m0);
+    k4_scale(hdr, 2 * kq + 1, sc1, m1);
+    const float d = g_h2f(hdr[0]), dm = g_h2f(hdr[0] >> 16);
+    const float dl0 = d * (float)sc0, b0 = -(dm * (float)m0), dl1 = d * (float)sc1, b1 = -(dm * (float)m1);
+    {
+      cvt4(q[i] & 0x0F0F0F0Fu, dl0, b0, o + 2 * i);
+      cvt4((q[i] >> 4) & 0x0F0F0F0Fu, dl1, b1, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q5_K> {
+  uint32_t q[4], qh[4], hdr[4];
+  static __device__ int off0(int h) { return 16 * h; }
+  static __device__ int off1(int h) { return 32 + 16 * h; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * kq + h)); gld<16>(qh, col16(c + 64 * 128, r, h)); gld<16>(hdr, c + 64 * 160 + r * 16);
+  }
+  __device__ void out(int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    int sc0, m0, sc1, m1;
+    k4_scale(hdr, 2 * kq, sc0, m0);
+    k4_scale(hdr, 2 * kq + 1, sc1, m1);
+    const float d = g_h2f(hdr[0]), dm = g_h2f(hdr[0] >> 16);
+    const float dl0 = d * (float)sc0, b0 = -(dm * (float)m0), dl1 = d * (float)sc1, b1 = -(dm * (float)m1);
+    {
+      cvt4((q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq)) & 0x01010101u) << 4), dl0, b0, o + 2 * i);
+      cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq + 1)) & 0x01010101u) << 4), dl1, b1, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_Q6_K> {   // groups 2 kq (ql bytes 64n + l) and 2 kq + 1 (64n + 32 + l), l = 16h + i
+  uint32_t a[4], b[4], qh[4], scw, d;
+  static __device__ int off0(int h) { return 16 * h; }
+  static __device__ int off1(int h) { return 32 + 16 * h; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    const int n = kq >> 1;
+    gld<16>(a, col16(c, r, 4 * n + h)); gld<16>(b, col16(c, r, 4 * n + 2 + h));
+    gld<16>(qh, col16(c + 64 * 128, r, 2 * n + h));
+    gld<4>(&scw, c + 64 * 192 + r * 16 + 4 * kq); gld<2>(&d, c + 64 * 208 + r * 2);
+  }
+  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+    const float dd = g_h2f(d);
+    const float dl0 = dd * (float)(int8_t)((scw >> (8 * h)) & 0xFF), dl1 = dd * (float)(int8_t)((scw >> (8 * (2 + h))) & 0xFF);
+    const int s = 4 * (kq & 1), t0 = 2 * (kq & 1);
+    {
+      const uint32_t u0 = ((a[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0)) & 0x03030303u) << 4);
+      const uint32_t u1 = ((b[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0 + 2)) & 0x03030303u) << 4);
+      cvt4(u0, dl0, -32.f * dl0, o + 2 * i);
+      cvt4(u1, dl1, -32.f * dl1, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_IQ4_XS> {
+  uint32_t q[4], hdr[2];
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    gld<16>(q, col16(c, r, 2 * kq + h)); gld<8>(hdr, c + 64 * 128 + r * 8);
+  }
+  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    const int g = 2 * kq + h;
+    const int ls = (int)(((hdr[1] >> (4 * g)) & 0xF) | (((hdr[0] >> (16 + 2 * g)) & 3) << 4));
+    const float dl = g_h2f(hdr[0]) * (float)(ls - 32);
+    {
+      cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), dl, -128.f * dl, o + 2 * i);
+      cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), dl, -128.f * dl, o + 8 + 2 * i);
+    }
+  }
+};
+
+template <> struct B2<GQK_IQ3_S> {   // group g = 2 kq + h: 32 weights, magnitudes from the grid, signs as bf16 masks
+  uint32_t qs[2], sg, qh[2], scb, d;
+  static __device__ int off0(int h) { return 32 * h; }
+  static __device__ int off1(int h) { return 32 * h + 16; }
+  __device__ void load(const uint8_t* c, int r, int kq, int h) {
+    const int g = 2 * kq + h;
+    gld<8>(qs, col16(c, r, g >> 1) + 8 * (g & 1));
+    gld<4>(&sg, col16(c + 64 * 64, r, g >> 2) + 4 * (g & 3));
+    gld<8>(qh, c + 64 * 96 + r * 8);
+    gld<4>(&scb, c + 64 * 104 + r * 4);
+    gld<2>(&d, c + 64 * 108 + r * 2);
+  }
+  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    const int g = 2 * kq + h;
+    const float dl = g_h2f(d) * (float)(1 + 2 * (int)((scb >> (4 * g)) & 0xF));
+    const uint32_t qhb = (uint32_t)(((uint64_t)qh[0] | ((uint64_t)qh[1] << 32)) >> (8 * g)) & 0xFF;
+    {
+      const int l = i;
+      const uint32_t qsw = qs[l >> 1] >> (16 * (l & 1));
+      const uint32_t i1 = (qsw & 0xFF) | ((qhb << (8 - 2 * l)) & 256);
+      const uint32_t i2 = ((qsw >> 8) & 0xFF) | ((qhb << (7 - 2 * l)) & 256);
+      const uint4 sm = tb.sign[(sg >> (8 * l)) & 0xFF];
+      uint32_t p[4];
+      cvt4(tb.grid[i1], dl, 0.f, p);
+      cvt4(tb.grid[i2], dl, 0.f, p + 2);
+      o[4 * l] = p[0] ^ sm.x; o[4 * l + 1] = p[1] ^ sm.y; o[4 * l + 2] = p[2] ^ sm.z; o[4 * l + 3] = p[3] ^ sm.w;
+    }
+  }
+};
+
+// LDS bytes of the 256 form: x and weight tiles, double-buffered, then the IQ3_S tables
+#define GB_TILE_BYTES (2 * (GB_M + GB_N) * GB_LD * 2)
+#define GB_TAB_BYTES (512 * 4 + 256 * 16)
+
+// Where a tile's accumulators go: straight to y (part == nullptr), or - for a tile whose k-steps
+// are shared by several workgroups (stream-K) - to this workgroup's fp32 partial slot, the last
+// contributor to arrive summing every slot in k order (deterministic) and writing y.
+struct GOut {
+  float* part;   // partial slots, 256 x 256 fp32 each
+  int* ctr;      // the tile's arrival counter (zero at rest, reset by the last contributor)
+  int slot0;     // slot of the tile's first contributor
+  int nc;        // contributors
+  int self;      // this workgroup's index among them
+};
+
+#define GB_SLOT_FLOATS (GB_M * GB_N)
+
+template <int T>
+__device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
+                                              const uint16_t* __restrict__ x, int64_t ldx, int M, int m0, int k0,
+                                              int k1, const GOut& go, uint16_t* __restrict__ y, int64_t ldy,
+                                              uint16_t* As, uint16_t* Bs, int* flag, const GTabs& tb) {
+  constexpr int REC = gqk_layout<T>::REC;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 3, wn = wave >> 2;
+  const int nb = dsc[D_NB], ntiles = dsc[D_NTILES];
+  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
+  const int64_t tile0 = dsc[D_TILE0];
+
+  // weight role: row br of the 256-row block, part h of the step's 64 weights
+  const int br = tid >> 1, h = tid & 1;
+  const int btile = br >> 6, brow = br & 63;
+  const uint8_t* bbase = packed + off + (tile0 + (btile < ntiles ? btile : 0)) * nb * (int64_t)(64 * REC);
+  // activation role: token ar of the block, 32 of the step's 64 k
+  const int ar = tid >> 1, ah = tid & 1;
+  const uint16_t* abase = x + (int64_t)min(m0 + ar, M - 1) * ldx + 32 * ah;
+
+  v16f acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Software pipeline over the k-steps [k0, k1): at step s the MFMAs read LDS buffer (s - k0) & 1
+  // while the same wave decodes the weights of step s + 1 (loaded one step earlier) into the other
+  // buffer, a quarter after each 16-k slice of MFMAs, and the loads of step s + 2's weights and
+  // step s + 1's activations are in flight.  One barrier per step.  Loads are unconditional
+  // (clamped to the last step).  Rows past M (x) and past the shard's rows (weights) hold clamped
+  // copies of real data: they only reach accumulator entries that are never stored.
+  const int last = k1 - 1;
+  uint4 av[4];
+  B2<T> p0, p1;
+  auto xload = [&](int s) {
+    const uint4* ap = (const uint4*)(abase + (int64_t)s * GB_K);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) av[i] = ap[i];
+  };
+  auto xstore = [&](int buf) {
+    uint4* as = (uint4*)(As + (buf * GB_M + ar) * GB_LD + 32 * ah);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) as[i] = av[i];
+  };
+  auto wload = [&](B2<T>& p, int s) { p.load(bbase + (int64_t)(s >> 2) * (64 * REC), brow, s & 3, h); };
+  auto wdecode = [&](const B2<T>& p, int s, uint32_t (&o)[16], int i) { p.out(s & 3, h, o, tb, i); };
+  auto wstore = [&](const uint32_t (&o)[16], int buf) {
+    uint16_t* bs = Bs + (buf * GB_N + br) * GB_LD;
+    uint4* d0 = (uint4*)(bs + B2<T>::off0(h));
+    uint4* d1 = (uint4*)(bs + B2<T>::off1(h));
+    d0[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    d0[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    d1[0] = make_uint4(o[8], o[9], o[10], o[11]);
+    d1[1] = make_uint4(o[12], o[13], o[14], o[15]);
+  };
+  auto step = [&](int s, const B2<T>& pd, B2<T>& pl) {
+    const int buf = (s - k0) & 1;
+    xload(min(s + 1, last));
+    wload(pl, min(s + 2, last));
+    const uint16_t* as = As + (buf * GB_M + wm * 64 + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    const uint16_t* bs = Bs + (buf * GB_N + wn * 128 + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    uint32_t o[16];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      v8bf af[2], bf[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = *(const v8bf*)(as + 32 * i * GB_LD + 16 * kk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = *(const v8bf*)(bs + 32 * j * GB_LD + 16 * kk);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      wdecode(pd, s + 1, o, kk);
+    }
+    xstore(buf ^ 1);
+    wstore(o, buf ^ 1);
+    __syncthreads();
+  };
+
+  xload(k0);
+  wload(p0, k0);
+  wload(p1, min(k0 + 1, last));
+  {
+    uint32_t o[16];
+    xstore(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wdecode(p0, k0, o, i);
+    wstore(o, 0);
+  }
+  __syncthreads();
+  int s = k0;
+  for (; s + 1 < k1; s += 2) {
+    step(s, p1, p0);
+    step(s + 1, p0, p1);
+  }
+  if (s < k1) step(s, p1, p0);
+
+  // C block (i, j): lane -> weight row 32 j + (lane & 31), tokens 8 (v / 4) + 4 (lane / 32) + v % 4
+  const int nvalid = dsc[D_NVALID];
+  const int64_t col0 = dsc[D_COL0];
+  auto store_y = [&](int i, int j, const v16f& a) {
+    const int r = wn * 128 + 32 * j + (lane & 31);
+    if (r >= nvalid) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int t = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (t < M) y[(int64_t)t * ldy + col0 + r] = __builtin_bit_cast(uint16_t, (__bf16)a[v]);
+    }
+  };
+  if (go.part == nullptr) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) store_y(i, j, acc[i][j]);
+    return;
+  }
+  // Partial slot layout: chunk c (16 bytes: elements 4 (c & 3) .. of acc[c >> 4][(c >> 2) & 3]) of
+  // thread tid at ((slot * 32 + c) * 512 + tid) * 16, so every store and load is coalesced.
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(go.part + (int64_t)go.slot0 * GB_SLOT_FLOATS, 0, go.nc * GB_SLOT_FLOATS * 4,
+                                        GQK_GB_WORD3);
+#pragma unroll
+  for (int c = 0; c < 32; ++c) {
+    const v16f& a = acc[c >> 4][(c >> 2) & 3];
+    const v4f q = {a[4 * (c & 3)], a[4 * (c & 3) + 1], a[4 * (c & 3) + 2], a[4 * (c & 3) + 3]};
+    __builtin_amdgcn_raw_buffer_store_b128(q, rs, ((go.self * 32 + c) * 512 + tid) * 16, 0, GQK_GB_SC1);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this workgroup's partial is complete
+  __syncthreads();
+  if (tid == 0) *flag = __hip_atomic_fetch_add(go.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*flag != go.nc - 1) return;
+  asm volatile("" ::: "memory");
+  // the last contributor: slot 0 + slot 1 + ... in k order, one 32 x 32 block (acc[i][j]) at a time
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c0 = 16 * i + 4 * j;
+      v4f sum[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((c0 + e) * 512 + tid) * 16, 0, GQK_GB_SC1);
+      for (int q = 1; q < go.nc; ++q) {
+        v4f t[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          t[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((q * 32 + c0 + e) * 512 + tid) * 16, 0, GQK_GB_SC1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += t[e];
+      }
+      const v16f a = {sum[0][0], sum[0][1], sum[0][2], sum[0][3], sum[1][0], sum[1][1], sum[1][2], sum[1][3],
+                      sum[2][0], sum[2][1], sum[2][2], sum[2][3], sum[3][0], sum[3][1], sum[3][2], sum[3][3]};
+      store_y(i, j, a);
+    }
+  if (tid == 0) __hip_atomic_store(go.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+}
+
+// Tile t -> (descriptor row, 256-token block).  Groups of up to eight token blocks take
+// consecutive tile ids, so with tiles dealt round robin to the workgroups and the dispatcher's
+// round robin over the eight XCDs, each XCD keeps one token block (256 x K activations) hot in
+// its L2 while the weight blocks stream by.
+__device__ __forceinline__ void gb_map(int i, int n_desc, int nmb, int& d, int& mb) {
+  const int full = (nmb / 8) * 8 * n_desc;
+  if (i < full) {
+    const int grp = i / (8 * n_desc), r = i % (8 * n_desc);
+    mb = grp * 8 + (r & 7);
+    d = r >> 3;
+  } else {
+    const int rem = nmb % 8, r = i - full;
+    mb = (nmb / 8) * 8 + r % rem;
+    d = r / rem;
+  }
+}
+
+// Persistent schedule over G workgroups (one per CU): the first floor(T / G) * G tiles whole,
+// dealt round robin; the remaining R tiles' k-steps split evenly over G_sk = min(G, R * steps)
+// workgroups (stream-K), tiles shared by several workgroups combined through partial slots.
+template <int ONLY>
+__global__ __launch_bounds__(512) void gemm_big_kernel(const uint8_t* __restrict__ packed,
+                                                       const int32_t* __restrict__ desc, int n_desc,
+                                                       const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                       uint16_t* __restrict__ y, int64_t ldy, float* part, int* ctr,
+                                                       int G) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[GB_TILE_BYTES + GB_TAB_BYTES + 16];
+  uint16_t* As = (uint16_t*)lds;
+  uint16_t* Bs = As + 2 * GB_M * GB_LD;
+  int* flag = (int*)(lds + GB_TILE_BYTES + GB_TAB_BYTES);
+  GTabs tb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tb.kv[i] = (uint32_t)(c_kvalues[4 * i] + 128) | ((uint32_t)(c_kvalues[4 * i + 1] + 128) << 8) |
+               ((uint32_t)(c_kvalues[4 * i + 2] + 128) << 16) | ((uint32_t)(c_kvalues[4 * i + 3] + 128) << 24);
+  uint32_t* grid = (uint32_t*)(lds + GB_TILE_BYTES);
+  uint4* sign = (uint4*)(lds + GB_TILE_BYTES + 512 * 4);
+  tb.grid = grid;
+  tb.sign = sign;
+  if (ONLY == 0 || ONLY == GQK_IQ3_S) {
+    const int t = threadIdx.x;
+    grid[t] = c_iq3s_grid[t];
+    if (t < 256) {
+      uint32_t m[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) m[p] = (((t >> (2 * p)) & 1) << 15) | (((t >> (2 * p + 1)) & 1) << 31);
+      sign[t] = make_uint4(m[0], m[1], m[2], m[3]);
+    }
+    __syncthreads();
+  }
+  const int nmb = (M + GB_M - 1) / GB_M;
+  const int T = n_desc * nmb;
+  const int nsteps = 4 * desc[D_NB];
+  auto run = [&](int t, int k0, int k1, const GOut& go) {
+    int d, mb;
+    gb_map(t, n_desc, nmb, d, mb);
+    const int32_t* dsc = desc + (int64_t)d * GQK_DESC_WORDS;
+    const int type = dsc[D_TYPE];
+#define RUN(TY)                                                                                          \
+    if ((ONLY == 0 || ONLY == TY) && type == TY)                                                         \
+      gemm_big_tile<TY>(packed, dsc, x, ldx, M, mb * GB_M, k0, k1, go, y, ldy, As, Bs, flag, tb);
+    RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
+    RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
+#undef RUN
+  };
+  const int tfull = (T / G) * G;
+  const int R = T - tfull;
+  const int64_t I = (int64_t)R * nsteps;
+  const int gsk = (int)min<int64_t>(G, I);
+  const int w = blockIdx.x;
+  auto owner = [&](int64_t i) { return (int)(((i + 1) * gsk + I - 1) / I - 1); };   // workgroup of step i
+  int64_t it = 0, end = 0;
+  if (R > 0 && w < gsk) {
+    it = (int64_t)w * I / gsk;
+    end = (int64_t)(w + 1) * I / gsk;
+  }
+  // one call site: whole tiles w, w + G, ... first, then this workgroup's stream-K steps
+  for (int t_dp = w;;) {
+    int t, k0, k1;
+    GOut go{nullptr, nullptr, 0, 1, 0};
+    if (t_dp < tfull) {
+      t = t_dp;
+      k0 = 0;
+      k1 = nsteps;
+      t_dp += G;
+    } else if (it < end) {
+      const int r = (int)(it / nsteps);
+      k0 = (int)(it % nsteps);
+      k1 = (int)min<int64_t>(nsteps, k0 + (end - it));
+      t = tfull + r;
+      if (k0 != 0 || k1 != nsteps) {
+        const int wf = owner((int64_t)r * nsteps), wl = owner((int64_t)r * nsteps + nsteps - 1);
+        go = GOut{part, ctr + r, r + wf, wl - wf + 1, w - wf};
+      }
+      it += k1 - k0;
+    } else {
+      break;
+    }
+    run(t, k0, k1, go);
+  }
+}
+
+// CUs of the current device (one 256 x 256 workgroup fits per CU), cached per device
+static int gb_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+int64_t gemm_big_workspace(int n_desc, int M, int nb) {
+  const int G = gb_cus();
+  if (G <= 0) return -1;
+  const int64_t T = (int64_t)n_desc * ((M + GB_M - 1) / GB_M);
+  const int64_t R = T % G;
+  if (R == 0) return 0;
+  const int64_t gsk = std::min<int64_t>(G, R * 4 * nb);
+  return (G * 4 + 255) / 256 * 256 + (R + gsk - 1) * GB_SLOT_FLOATS * 4;
+}
+
+static int launch_big(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
+                      const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, void* ws, int64_t ws_bytes) {
+  const int G = gb_cus();
+  if (G <= 0) return GQK_ERR_HIP;
+  const int64_t need = gemm_big_workspace(n_desc, M, nb);
+  if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255))) return GQK_ERR_SHAPE;
+  int* ctr = (int*)ws;
+  float* part = need > 0 ? (float*)((char*)ws + (G * 4 + 255) / 256 * 256) : nullptr;
+  // G workgroups when there are at least G tiles; else every stream-K participant,
+  // min(G, T * steps) (the kernel splits the steps of all T tiles over that many)
+  const int64_t T = (int64_t)n_desc * ((M + GB_M - 1) / GB_M);
+  dim3 grid((unsigned)(T >= G ? G : std::min<int64_t>(G, T * 4 * nb)));
+  switch (only) {
+#define C(T) case T: hipLaunchKernelGGL((gemm_big_kernel<T>), grid, dim3(512), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G); return GQK_OK;
+    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
+    default:
+      hipLaunchKernelGGL((gemm_big_kernel<0>), grid, dim3(512), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G);
+  }
+  return GQK_OK;
+}
+
 template <int BM>
 static void launch_bm(int only, dim3 grid, hipStream_t st, const uint8_t* packed, const int32_t* desc, const uint16_t* x,
                       int64_t ldx, int M, uint16_t* y, int64_t ldy) {
@@ -453,10 +1059,12 @@ static void launch_bm(int only, dim3 grid, hipStream_t st, const uint8_t* packed
 }
 
 int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int64_t K, void* y, int64_t ldy, int bm, hipStream_t st) {
-  (void)K;
+                int M, int64_t K, void* y, int64_t ldy, int bm, void* ws, int64_t ws_bytes, hipStream_t st) {
   dim3 grid(n_desc, (M + bm - 1) / bm);
-  if (bm == 128)
+  if (bm == 256)
+    return launch_big(types_mask, n_desc, M, (int)(K / 256), st, packed, desc, (const uint16_t*)x, ldx, (uint16_t*)y, ldy,
+                      ws, ws_bytes);
+  else if (bm == 128)
     launch_bm<128>(types_mask, grid, st, packed, desc, (const uint16_t*)x, ldx, M, (uint16_t*)y, ldy);
   else if (bm == 64)
     launch_bm<64>(types_mask, grid, st, packed, desc, (const uint16_t*)x, ldx, M, (uint16_t*)y, ldy);

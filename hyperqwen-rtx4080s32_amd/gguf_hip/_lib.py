@@ -22,7 +22,7 @@ GQK_DTYPE_F32, GQK_DTYPE_BF16, GQK_DTYPE_F16 = 0, 1, 2
 
 # every entry point include/gguf_hip.h declares
 EXPORTS = ("gqk_last_error", "gqk_version", "gqk_type_info", "gqk_dequantize", "gqk_tiles_bytes", "gqk_repack",
-           "gqk_unrepack", "gqk_plan", "gqk_linear")
+           "gqk_unrepack", "gqk_plan", "gqk_linear_workspace_bytes", "gqk_linear")
 
 
 class GqkShard(ctypes.Structure):
@@ -68,6 +68,7 @@ def _load() -> ctypes.CDLL:
         "gqk_unrepack": (i32, [vp, i32, i64, i64, vp, i64, vp]),
         "gqk_plan": (i32, [ctypes.POINTER(GqkShard), i32, i64, i32, i32, ctypes.POINTER(ctypes.c_int32), i64,
                            ctypes.POINTER(GqkPlanInfo)]),
+        "gqk_linear_workspace_bytes": (i64, [ctypes.POINTER(GqkPlanInfo), i32]),
         "gqk_linear": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, i64, vp]),
     }
     for name, (res, args) in sig.items():

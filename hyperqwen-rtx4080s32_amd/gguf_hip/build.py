@@ -1,6 +1,7 @@
 """Builds the HIP library ``libgqk.so`` in-tree for gfx950 (hipcc, no JIT cache).
 
-    python -m gguf_hip.build          # from hyperqwen-rtx4080s32_amd/
+    python hyperqwen-rtx4080s32_amd/gguf_hip/build.py     # as a script: no package import, so a
+                                                          # stale or missing library is no obstacle
 """
 from __future__ import annotations
 

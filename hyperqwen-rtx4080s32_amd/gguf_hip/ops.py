@@ -34,7 +34,7 @@ UNQUANTIZED_TYPES = (0, 1, 30)
 
 # batch-row buckets of a grouped layer: GEMV plans serve M <= 4, 8, 16, 32; GEMM above
 GEMV_BUCKETS = (4, 8, 16, 32)
-GEMM_PLAN_M = (64, 65)   # a bm-64 plan (33..64 rows) and a bm-128 plan (65+ rows)
+GEMM_PLAN_M = (64, 128, 129)   # GEMM plans: bm 64 (33..64 rows), bm 128 (65..128), 256 x 256 tiles (129+)
 
 _DTYPES = {torch.float32: _lib.GQK_DTYPE_F32, torch.bfloat16: _lib.GQK_DTYPE_BF16, torch.float16: _lib.GQK_DTYPE_F16}
 
@@ -221,7 +221,10 @@ def _pick_plan(plans: list[int], M: int) -> int:
     for i, m in enumerate(GEMV_BUCKETS):
         if M <= m:
             return i
-    return len(GEMV_BUCKETS) + (0 if M <= GEMM_PLAN_M[0] else 1)
+    for i, m in enumerate(GEMM_PLAN_M[:-1]):
+        if M <= m:
+            return len(GEMV_BUCKETS) + i
+    return len(GEMV_BUCKETS) + len(GEMM_PLAN_M) - 1
 
 
 def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
@@ -253,6 +256,20 @@ def _(x, packed, descs, plans, n_total, workspace):
     return torch.empty((x.shape[0], n_total), dtype=torch.bfloat16, device=x.device)
 
 
+def _ensure_workspace(gl: GroupedLayer, M: int) -> None:
+    """Grow the layer's workspace (zero-filled, as the counters need) to what the plan serving M
+    rows needs.  GEMV plans are covered at preparation; the large-M GEMM's stream-K partials
+    depend on M, so the first call at a larger M grows it (outside any graph capture)."""
+    if M <= 0:
+        return
+    i = _pick_plan(gl.plans, M)
+    info = GqkPlanInfo.from_tuple(gl.plans[i * _NPLAN:(i + 1) * _NPLAN])
+    need = check(lib.gqk_linear_workspace_bytes(ctypes.byref(info), M), "linear_workspace_bytes")
+    have = gl.workspace.numel() * gl.workspace.element_size()
+    if need > have:
+        gl.workspace = torch.zeros((need + 3) // 4, dtype=torch.int32, device=gl.packed.device)
+
+
 def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer) -> torch.Tensor:
     """y = x @ W^T for a prepared grouped layer, in x's dtype.  The kernels take bf16
     activations; other floating dtypes are rounded to bf16 on the way in and the bf16 result
@@ -263,6 +280,7 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer) -> torch.Tensor:
     xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
     if xb.stride(1) != 1 or xb.stride(0) % 8 or xb.data_ptr() % 16:
         xb = xb.contiguous()
+    _ensure_workspace(gl, int(xb.shape[0]))
     y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace)
     return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
 

@@ -96,12 +96,18 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
 int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
              int64_t desc_capacity, gqk_plan_info* info);
 
+/* Device workspace bytes gqk_linear needs for this plan at M batch rows (0: none; < 0: error).
+ * GEMV plans with split-K need info->workspace_bytes; the 256-token GEMM form (info->bm == 256)
+ * needs room for its stream-K partial tiles, which depends on M and on the current device's CU
+ * count.  Replaces the reference's transient split-K partials (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
+int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
+
 /* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T over the grouped layer's shards (columns in shard
- * order), on `stream`.  desc_dev: the plan's descriptor table in device memory.  workspace: when
- * info->split > 1, at least info->workspace_bytes of 256-byte aligned device memory holding the
- * split-K arrival counters (first) and fp32 partials; it must be zero-filled before its first
- * use, every launch leaves the counters at zero again, and launches sharing one workspace must
- * not overlap in time (else NULL).  M must be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
+ * order), on `stream`.  desc_dev: the plan's descriptor table in device memory.  workspace: at
+ * least gqk_linear_workspace_bytes(info, M) bytes of 256-byte aligned device memory (NULL when
+ * that is 0) holding arrival counters (first) and fp32 partials; it must be zero-filled before
+ * its first use, every launch leaves the counters at zero again, and launches sharing one
+ * workspace must not overlap in time.  M must be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,

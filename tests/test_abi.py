@@ -103,10 +103,15 @@ def test_plan_descriptor_rows_mixed_layer():
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
     assert d[:, 8].tolist() == [0, 64, 70, 134, 198, 262, 326] and d[:, 9].tolist() == [64, 6, 64, 64, 64, 64, 44]
     assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 11].tolist() == list(range(7))
+    gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 100)
+    g = _rows(gd)
+    assert gi.form == 2 and gi.bm == 128 and g.shape[0] == 1 + 3          # two tiles per row
+    assert g[:, 4].tolist() == [2, 2, 2, 1] and g[:, 6].tolist() == [3] * 4
     gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 2048)
     g = _rows(gd)
-    assert gi.form == 2 and gi.bm == 128 and g.shape[0] == 1 + 3
-    assert g[:, 4].tolist() == [2, 2, 2, 1] and g[:, 6].tolist() == [3] * 4
+    assert gi.form == 2 and gi.bm == 256 and g.shape[0] == 1 + 2          # four tiles per row
+    assert g[:, 4].tolist() == [2, 4, 1] and g[:, 9].tolist() == [70, 256, 44]
+    assert g[:, 8].tolist() == [0, 70, 326]
     assert ops.plan([(21, 70, 0), (12, 300, off2)], K, 40)[0].bm == 64
 
 
@@ -118,3 +123,6 @@ def test_plan_buckets():
         assert info.form == 1 and info.g == g and info.m_max == 4 * g
     assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 32) == 3
     assert ops._pick_plan([], 33) == 4 and ops._pick_plan([], 64) == 4 and ops._pick_plan([], 65) == 5
+    assert ops._pick_plan([], 128) == 5 and ops._pick_plan([], 129) == 6 and ops._pick_plan([], 8192) == 6
+    for M, bm in ((33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
+        assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm

@@ -200,3 +200,27 @@ def test_baseline_config1_q8_0(dev):
     gl = gguf_hip.pack_layer([Wd], [N], [G.Q8_0])
     e = G.rel_err(gguf_hip.mul_mat_grouped(x, gl).float().cpu().numpy(), _ref(x, wf))
     assert e < TOL, e
+
+
+@pytest.mark.parametrize("n,K,M", [(1000, 2048, 300), (1000, 2048, 2148), (16384, 512, 1100)], ids=str)
+def test_gemm_stream_k_schedule(dev, n, K, M):
+    """The 256 x 256 GEMM's persistent schedule: whole tiles dealt to the CUs, the remainder
+    tiles' k-steps split over all of them (stream-K) and combined in k order by the last
+    contributor.  Small grids are all remainder, the 16384-row case mixes both phases.  Checked
+    against an fp32 matmul of the GPU-dequantized weights (pinned bit-exact by the dequant
+    tests), repeated launches bit-identical, counters back at zero."""
+    import gguf_hip
+    from gguf_hip.synth import random_shard
+
+    W = random_shard(n, K, G.Q5_K, dev, seed=n + M)
+    wf = gguf_hip.dequantize(W, G.Q5_K, (n, K), torch.float32)
+    gl = gguf_hip.pack_layer([W], [n], [G.Q5_K])
+    x = torch.randn(M, K, device=dev, generator=torch.Generator(device=dev).manual_seed(M)).to(torch.bfloat16)
+    y = gguf_hip.mul_mat_grouped(x, gl)
+    ref = x.float() @ wf.T
+    scale = ref.abs().amax(dim=1, keepdim=True).clamp(min=1e-30)
+    assert float(((y.float() - ref).abs() / scale).amax()) < TOL
+    for _ in range(3):
+        assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y)
+    torch.cuda.synchronize()
+    assert int(gl.workspace[:256].abs().sum()) == 0            # the arrival counters
