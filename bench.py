@@ -215,9 +215,11 @@ def main() -> int:
         g = _capture(f, torch)
         g.replay()
         t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (4 * len(gls))
-        plan = gls[0].plans[[4, 8, 16, 32].index(next(b for b in (4, 8, 16, 32) if M <= b)) * 10:][:10]
+        info = gguf_hip.ops.GqkPlanInfo.from_tuple(
+            gls[0].plans[gguf_hip.ops._pick_plan(gls[0].plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
-                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": plan[2], "split": plan[4], "wgs": plan[5]})
+                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
+                     "waves_per_wg": info.nw})
         del g
     dom = max(rows, key=lambda r: r["us"])
     dom_wt = next(s[0] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])

@@ -30,10 +30,12 @@ int check_launch(const char* what) {
   return GQK_OK;
 }
 
-// GEMV workgroup target when the caller gives none: two 4-wave workgroups per CU of a 256-CU
-// MI355X.  Small shards split K to reach it; large ones (>= 512 tiles) run one workgroup per
-// tile, all resident at once (a second generation of workgroups costs more than it hides).
-constexpr int kDefaultTargetWgs = 512;
+// GEMV wave target when the caller gives none: eight waves per CU of a 256-CU MI355X.  A
+// workgroup takes one 64-row tile and up to four waves split its k-range (measured: more waves
+// per workgroup, or more waves than stay resident at once, run slower); shards with too few
+// tiles for the target also split K across workgroups (partials combined in-kernel).
+constexpr int kDefaultTargetWaves = 2048;
+constexpr int kGemvWaves = 4;
 
 // bytes of the split-K arrival counters of `tiles` tiles (rounded to 256 so the partials stay aligned)
 int64_t gqk_counter_bytes(int64_t tiles) { return (tiles * 4 + 255) / 256 * 256; }
@@ -164,20 +166,22 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   };
   int64_t tiles = 0;
   for (int i = 0; i < nshards; ++i) tiles += (shards[i].n + 63) / 64;
-  if (M <= 32) {
+  if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
 #ifdef GQK_GEMV_MIN_G
     pi.g = std::max(pi.g, GQK_GEMV_MIN_G);
 #endif
     pi.m_max = 4 * pi.g;
-    // one workgroup per (tile, k-range), its four waves taking quarters of the k-range: enough
-    // workgroups to fill the chip, each wave keeping >= 2 super-blocks where the shape allows
-    const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWgs;
-    int64_t split = (target + tiles - 1) / tiles;
-    int64_t cap = std::max<int64_t>(1, nb / 8);
-    if (tiles * cap < 512) cap = std::max<int64_t>(1, nb / 4);
-    split = std::max<int64_t>(1, std::min({split, cap, (int64_t)GQK_SPLIT_MAX}));
+    // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
+    // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
+    // workgroup holds does K split across workgroups.  Every wave keeps >= 1 super-block.
+    const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWaves;
+    const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
+    const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
+    const int64_t split =
+        std::max<int64_t>(1, std::min({(per_tile + nw - 1) / nw, nb / nw, (int64_t)GQK_SPLIT_MAX}));
+    pi.nw = (int32_t)nw;
     pi.split = (int32_t)split;
     int64_t col0 = 0, ctr = 0;
     for (int i = 0; i < nshards; ++i) {
@@ -256,13 +260,13 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
       counters = (int*)workspace;
       partials = (float*)((char*)workspace + cb);
     }
-    int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, y,
+    int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw, y,
                               ldy, partials, counters, info->split, info->n_total, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }
   if (info->form == GQK_FORM_GEMM) {
-    if (M <= 32) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
+    if (M <= GQK_GEMV_MAX_M) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
     if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
     int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
                               info->bm, workspace, workspace_bytes, (hipStream_t)stream);

@@ -112,6 +112,10 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 // descriptor row of a grouped launch (int32 words)
 #define GQK_DESC_WORDS 16
 #define GQK_SPLIT_MAX 16   // split-K factor bound: the last workgroup loads every partial at once
+#ifndef GQK_GEMV_MAX_M
+#define GQK_GEMV_MAX_M 32   // batch rows served by the GEMV form; the GEMM above
+#endif
+#define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
 enum {
   D_TYPE = 0,     // GGML type of the row's shard
   D_OFF_LO = 1,   // byte offset of the shard's tiles in the packed buffer (low 32 bits)

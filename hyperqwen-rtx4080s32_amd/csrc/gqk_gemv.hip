@@ -477,38 +477,42 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
   }
 }
 
+// The IQ lookup tables in LDS, built by all blockDim.x threads (any workgroup size).
 __device__ void build_tables(uint8_t* lds_tab, int type) {
-  const int tid = threadIdx.x;
+  const int nt = blockDim.x;
   if (type == GQK_IQ4_NL || type == GQK_IQ4_XS) {
-    uint32_t* t4 = (uint32_t*)lds_tab;
-    t4[tid] = bf16x2((float)c_kvalues[tid & 15], (float)c_kvalues[tid >> 4]);
+    uint32_t* t4 = (uint32_t*)lds_tab;                    // [256] bf16 pairs (kv[b & 15], kv[b >> 4])
+    for (int i = threadIdx.x; i < 256; i += nt) t4[i] = bf16x2((float)c_kvalues[i & 15], (float)c_kvalues[i >> 4]);
   } else if (type == GQK_IQ3_S) {
-    uint2* tg = (uint2*)lds_tab;
-    uint4* ts = (uint4*)(lds_tab + 512 * 8);
-    for (int i = tid; i < 512; i += 256) {
+    uint2* tg = (uint2*)lds_tab;                          // [512] grid magnitudes as bf16 x 4
+    uint4* ts = (uint4*)(lds_tab + 512 * 8);              // [256] sign masks of a sign byte
+    for (int i = threadIdx.x; i < 512; i += nt) {
       uint32_t gw = c_iq3s_grid[i];
       tg[i] = make_uint2(bf16x2((float)(gw & 0xFF), (float)((gw >> 8) & 0xFF)),
                          bf16x2((float)((gw >> 16) & 0xFF), (float)(gw >> 24)));
     }
-    uint32_t m[4];
+    for (int i = threadIdx.x; i < 256; i += nt) {
+      uint32_t m[4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) m[p] = (((tid >> (2 * p)) & 1) << 15) | (((tid >> (2 * p + 1)) & 1) << 31);
-    ts[tid] = make_uint4(m[0], m[1], m[2], m[3]);
+      for (int p = 0; p < 4; ++p) m[p] = (((i >> (2 * p)) & 1) << 15) | (((i >> (2 * p + 1)) & 1) << 31);
+      ts[i] = make_uint4(m[0], m[1], m[2], m[3]);
+    }
   }
 }
 
 #define GEMV_TAB_BYTES 9216
 
-// LDS of a workgroup: 4 wave-private x regions, then the IQ tables.
+// Dynamic LDS of a workgroup of nw waves: nw wave-private x regions, then the IQ tables.
 template <int G>
-__host__ __device__ constexpr int gemv_lds_bytes(bool tables) {
-  return 4 * WaveX<4 * G>::BYTES + (tables ? GEMV_TAB_BYTES : 0);
+__host__ __device__ constexpr int gemv_lds_bytes(int nw, bool tables) {
+  return nw * WaveX<4 * G>::BYTES + (tables ? GEMV_TAB_BYTES : 0);
 }
 
-// One workgroup per descriptor row: one 64-row tile, its k-range split over the 4 waves, the
-// waves' sums combined through LDS in a fixed order; with split-K (part != nullptr) the fp32
-// partial goes to part[split] and the last workgroup of the tile to arrive (counter ctr[tile])
-// sums the partials in split order and writes y, then resets the counter.
+// One workgroup of nw waves (blockDim.x / 64, at most GQK_GEMV_MAX_WAVES) per descriptor row: one
+// 64-row tile, its k-range split evenly over the waves, the waves' sums combined through LDS in
+// a fixed order; with split-K (part != nullptr) the fp32 partial goes to the tile's partial slot
+// and the last workgroup of the tile to arrive (counter ctr[tile]) sums the partials in split
+// order and writes y, then resets the counter.
 // Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 fits
 // three waves without spilling and runs faster there than at the allocator's own choice of two.
 template <int G, int ONLY>
@@ -521,16 +525,16 @@ constexpr int gemv_waves() {
 }
 
 template <int G, int ONLY>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>()))) void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
-                                                   const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                   uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
-                                                   int* __restrict__ ctr, int64_t n_total, int split) {
+__global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>())))
+void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
+                 int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
+                 int* __restrict__ ctr, int64_t n_total, int split) {
   constexpr int MPAD = 4 * G;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[gemv_lds_bytes<G>(true)];
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
   const int type = dsc[D_TYPE];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint8_t* lds_tab = lds + 4 * WaveX<MPAD>::BYTES;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  uint8_t* lds_tab = lds + nw * WaveX<MPAD>::BYTES;
   const bool iq = type == GQK_IQ4_NL || type == GQK_IQ4_XS || type == GQK_IQ3_S;
   Tabs tb{(const uint32_t*)lds_tab, (const uint2*)lds_tab, (const uint4*)(lds_tab + 4096)};
   if (iq) {
@@ -541,7 +545,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<
   const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
   const int64_t tile = dsc[D_TILE0];
   const int nb = dsc[D_NB], kb0 = dsc[D_KB0], nk = dsc[D_KB1] - kb0;
-  const int kw0 = kb0 + (wave * nk) / 4, kw1 = kb0 + ((wave + 1) * nk) / 4;
+  const int kw0 = kb0 + (wave * nk) / nw, kw1 = kb0 + ((wave + 1) * nk) / nw;
   uint8_t* wl = lds + wave * WaveX<MPAD>::BYTES;
   v4f acc[G];
 #pragma unroll
@@ -554,7 +558,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<
   RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
 
-  // combine the four waves (fixed order) in wave 0
+  // combine the waves (fixed order) in wave 0
   __syncthreads();                                  // every wave is done with its x region
   v4f* red = (v4f*)lds;                             // [wave][g][lane]
   if (wave > 0)
@@ -562,8 +566,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<
     for (int g = 0; g < G; ++g) red[(wave * G + g) * 64 + lane] = acc[g];
   __syncthreads();
   if (wave > 0) return;
-#pragma unroll
-  for (int w = 1; w < 4; ++w)
+  for (int w = 1; w < nw; ++w)
 #pragma unroll
     for (int g = 0; g < G; ++g) acc[g] += red[(w * G + g) * 64 + lane];
 
@@ -628,33 +631,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemv_waves<
 }
 
 template <int G>
-static void launch_g(int only, dim3 grid, hipStream_t st, const uint8_t* packed, const int32_t* desc,
+static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
                      const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, float* part, int* ctr,
                      int64_t n_total, int split) {
-  const size_t lds = 0;
+  const bool iq = only == 0 || only == GQK_IQ4_NL || only == GQK_IQ4_XS || only == GQK_IQ3_S;
+  const size_t lds = (size_t)gemv_lds_bytes<G>(nw, iq);
+  const dim3 block(64 * nw);
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, dim3(256), lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split); return;
+#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split); return;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, dim3(256), lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split);
+      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split);
   }
 }
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, void* y, int64_t ldy, float* partials, int* counters, int split, int64_t n_total,
+                int M, int G, int nw, void* y, int64_t ldy, float* partials, int* counters, int split, int64_t n_total,
                 hipStream_t st) {
+  if (nw < 1 || nw > GQK_GEMV_MAX_WAVES || (G == 8 && 2 * nw > GQK_GEMV_MAX_WAVES)) return GQK_ERR_FORM;
   dim3 grid(n_desc);
   float* part = split > 1 ? partials : nullptr;
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   switch (G) {
-    case 1: launch_g<1>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 2: launch_g<2>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 4: launch_g<4>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 8: launch_g<8>(types_mask, grid, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 8: launch_g<8>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
     default: return GQK_ERR_FORM;
   }
   return GQK_OK;

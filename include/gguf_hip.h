@@ -53,6 +53,8 @@ typedef struct gqk_plan_info {
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
   int32_t nb;         /* K / 256 */
+  int32_t nw;         /* GEMV: waves per workgroup (they split the workgroup's k-range) */
+  int32_t reserved;
   int64_t n_total;    /* output columns: sum of the shards' rows */
   int64_t workspace_bytes; /* device workspace gqk_linear needs (any M <= m_max) */
 } gqk_plan_info;
@@ -90,7 +92,8 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
 /* Host-only: the launch plan of a grouped layer (shards packed back to back, all of K columns)
  * for batch rows M: fills *info and, if desc is not NULL and desc_capacity (int32 words) is
  * enough, the descriptor table (16 int32 per row) to upload to the device.  target_wgs > 0
- * overrides the GEMV split heuristic's workgroup target (0 = default).  Replaces
+ * overrides the GEMV heuristic's target of resident waves (0 = default), from which the waves
+ * per workgroup and the split-K factor follow.  Replaces
  * prepare_grouped_layer / descriptors / grouped_split_for
  * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
 int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,

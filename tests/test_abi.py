@@ -74,19 +74,26 @@ def _rows(desc):
 def test_plan_gemv_balanced_split_partition():
     from gguf_hip import ops
 
-    for target in (16, 40, 97, 1024):
+    for target in (1, 16, 97, 1024, 4096, 0):
         info, desc = ops.plan([(21, 6144, 0)], 20 * 256, 1, target)
         d = _rows(desc)
-        S = info.split
+        S, nw = info.split, info.nw
         assert info.form == 1 and info.g == 1 and info.m_max == 4
-        assert d.shape[0] == info.n_desc == 96 * S        # one workgroup per (64-row tile, split)
-        first = d[d[:, 3] == 0]                          # the workgroups of tile 0
+        assert 1 <= nw <= 4 and S * nw <= 20                # every wave keeps >= 1 super-block
+        if S > 1:
+            assert nw == 4                                  # K splits across workgroups only past a full one
+        assert d.shape[0] == info.n_desc == 96 * S          # one workgroup per (64-row tile, split)
+        first = d[d[:, 3] == 0]                             # the workgroups of tile 0
         assert first[:, 5].tolist() == [s * 20 // S for s in range(S)]
         assert first[:, 6].tolist() == [(s + 1) * 20 // S for s in range(S)]
         assert first[:, 7].tolist() == list(range(S)) and (first[:, 11] == 0).all()
-        assert (first[:, 6] > first[:, 5]).all() and 1 <= S <= 5
         assert sorted(set(d[:, 11].tolist())) == list(range(96))   # one arrival counter per tile
         assert info.workspace_bytes == (512 + S * 4 * 6144 * 4 if S > 1 else 0)
+    assert ops.plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
+    info = ops.plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
+    assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
+    info = ops.plan([(21, 6144, 0)], 20 * 256, 8, 0)[0]
+    assert (info.nw, info.split) == (4, 5)                  # default target 2048 waves: 22 per tile
 
 
 def test_plan_descriptor_rows_mixed_layer():
@@ -103,6 +110,7 @@ def test_plan_descriptor_rows_mixed_layer():
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
     assert d[:, 8].tolist() == [0, 64, 70, 134, 198, 262, 326] and d[:, 9].tolist() == [64, 6, 64, 64, 64, 64, 44]
     assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 11].tolist() == list(range(7))
+    assert info.nw == 1                                     # a target of 4 waves for 7 tiles: one each
     gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 100)
     g = _rows(gd)
     assert gi.form == 2 and gi.bm == 128 and g.shape[0] == 1 + 3          # two tiles per row

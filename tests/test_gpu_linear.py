@@ -75,8 +75,8 @@ def test_split_k_repeat_is_bit_identical(dev):
     n, K = 1000, 40 * 256
     raw = G.random_blocks(rng, n, K, G.Q4_K)
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K], target_wgs=4096)
-    plan = gl.plans[:10]
-    assert plan[4] > 1, "the plan must split K"
+    info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[:gguf_hip.ops._NPLAN])
+    assert info.split > 1, "the plan must split K"
     wf = G.dequantize(raw, G.Q4_K)
     for M in (1, 8):
         x = _x(M, K, 7000 + M, dev)
