@@ -168,7 +168,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   for (int i = 0; i < nshards; ++i) tiles += (shards[i].n + 63) / 64;
   if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
-    pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
+    pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
 #ifdef GQK_GEMV_MIN_G
     pi.g = std::max(pi.g, GQK_GEMV_MIN_G);
 #endif
@@ -196,7 +196,8 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
-    // 64 / 128 tokens x 128 rows per workgroup up to 128 tokens; 256 x 256 above
+    // 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens on
+    // the GEMM outruns the GEMV's 4 x 4 x 4 MFMAs (one decode of each weight for up to 64 tokens).
     pi.bm = M <= 64 ? 64 : M <= 128 ? 128 : 256;
     pi.m_max = 1 << 30;
     pi.split = 1;
@@ -225,8 +226,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
   if (M <= 0) return 0;
   if (info->form == GQK_FORM_GEMV) return info->split > 1 ? info->workspace_bytes : 0;
   if (info->form == GQK_FORM_GEMM) {
-    if (info->bm != 256) return 0;
-    const int64_t n = gqk::gemm_big_workspace(info->n_desc, M, info->nb);
+    const int64_t n = gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb);
     return n < 0 ? fail(GQK_ERR_HIP, "linear_workspace_bytes: no HIP device") : n;
   }
   return fail(GQK_ERR_FORM, "linear_workspace_bytes: unknown form %d", info->form);
@@ -272,7 +272,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
                               info->bm, workspace, workspace_bytes, (hipStream_t)stream);
     if (rc == GQK_ERR_SHAPE)
       return fail(rc, "linear: GEMM workspace %lld bytes < %lld (or not 256-byte aligned)", (long long)workspace_bytes,
-                  (long long)gqk::gemm_big_workspace(info->n_desc, M, info->nb));
+                  (long long)gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb));
     if (rc) return fail(rc, "linear: GEMM launch form bm=%d", info->bm);
     return check_launch("linear (GEMM)");
   }

@@ -113,7 +113,7 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 #define GQK_DESC_WORDS 16
 #define GQK_SPLIT_MAX 16   // split-K factor bound: the last workgroup loads every partial at once
 #ifndef GQK_GEMV_MAX_M
-#define GQK_GEMV_MAX_M 32   // batch rows served by the GEMV form; the GEMM above
+#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form; the GEMM above
 #endif
 #define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
 enum {
@@ -132,5 +132,5 @@ enum {
 };
 
 // forms of a grouped launch
-#define GQK_FORM_GEMV 1   // M <= 32: in-register decode, MFMA 4x4x4 per sub-block, fp32 epilogue
-#define GQK_FORM_GEMM 2   // M > 32: tile decoded to bf16 in LDS, MFMA 32x32x16
+#define GQK_FORM_GEMV 1   // M <= 16: in-register decode, MFMA 4x4x4 per sub-block, fp32 epilogue
+#define GQK_FORM_GEMM 2   // M > 16: tile decoded to bf16 in LDS, MFMA 32x32x16

@@ -2,11 +2,12 @@
 //
 // Replaces the reference's prefill paths: the wide int8 forms of the grouped kernel and, for
 // Q4_K / Q5_K, dequantize_tiles + cuBLAS bf16 (gguf-plugin/gluon/interface.py:159-188,
-// gguf-plugin/gluon/tiles.py:141-149).  Here one kernel does both: each workgroup owns a
-// BM x 128 output tile (BM tokens, two 64-row weight tiles of one shard), walks K in steps of
-// 64, decodes the step's weights to bf16 in LDS (bf16 = round-to-nearest-even of the exact
+// gguf-plugin/gluon/tiles.py:141-149).  Here one persistent kernel does both: each workgroup
+// takes BM x BN output tiles (BM tokens, BN weight rows of one shard) in turn, walks K in steps
+// of 64, decodes the step's weights to bf16 in LDS (bf16 = round-to-nearest-even of the exact
 // fp32 gguf-py value), stages the activations beside them, and runs v_mfma_f32_32x32x16_bf16
-// with fp32 accumulation.  Global loads of step s+1 are in flight while step s multiplies.
+// with fp32 accumulation.  Tiles left over after whole rounds over the workgroups are split
+// along K (stream-K) and their partial sums combined in a fixed order.
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include "gqk_common.h"
@@ -28,7 +29,6 @@ __device__ __forceinline__ uint32_t g_bf16x2(float lo, float hi) {
   p[1] = (__bf16)hi;
   return __builtin_bit_cast(uint32_t, p);
 }
-__device__ __forceinline__ uint32_t g_byte(const uint32_t* w, int b) { return (w[b >> 2] >> (8 * (b & 3))) & 0xFF; }
 
 template <int N>
 __device__ __forceinline__ void gld(uint32_t* dst, const uint8_t* p) {
@@ -55,402 +55,15 @@ __device__ __forceinline__ void gld(uint32_t* dst, const uint8_t* p) {
 // 16-byte column `col` of row r in a plane with 16-byte columns (column-major: (col * 64 + r) * 16)
 __device__ __forceinline__ const uint8_t* col16(const uint8_t* plane, int r, int col) { return plane + (col * 64 + r) * 16; }
 
-// Per-type decode of one group of 32 consecutive weights (g = 0..7 of a super-block) of row r
-// to 16 dwords of bf16 pairs in natural k order.  load() issues the global loads, out() decodes.
-template <int T> struct GDec;
+// ---- tile forms ------------------------------------------------------------------------------
+// A workgroup owns BM tokens x BN weight rows (BN / 64 tiles of one shard) and walks K in steps of
+// 64.  Forms: 256 x 256 with 8 waves (two per SIMD, one workgroup per CU: M > 128), and 128 x 128 /
+// 64 x 128 with 4 waves (two workgroups per CU: M 65..128 / 33..64).  Each wave owns a block of
+// 32 x 32 v_mfma_f32_32x32x16_bf16 outputs.  Per step each thread decodes 32 weights of one row
+// (two runs of 16 at step-local offsets OFF0 / OFF1, per type) and stages activations of one
+// token; the next steps' loads are in flight during the MFMAs.  LDS: x and weights
+// double-buffered plus the IQ3_S tables.
 
-template <> struct GDec<GQK_Q4_0> {
-  uint32_t qs[4], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, g)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
-  __device__ void out(uint32_t* o) const {
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      uint32_t b0 = g_byte(qs, j), b1 = g_byte(qs, j + 1);
-      o[j / 2] = g_bf16x2(dd * (float)((int)(b0 & 0xF) - 8), dd * (float)((int)(b1 & 0xF) - 8));
-      o[8 + j / 2] = g_bf16x2(dd * (float)((int)(b0 >> 4) - 8), dd * (float)((int)(b1 >> 4) - 8));
-    }
-  }
-};
-
-template <> struct GDec<GQK_IQ4_NL> {
-  uint32_t qs[4], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, g)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * g); }
-  __device__ void out(uint32_t* o) const {
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      uint32_t b0 = g_byte(qs, j), b1 = g_byte(qs, j + 1);
-      o[j / 2] = g_bf16x2(dd * (float)c_kvalues[b0 & 0xF], dd * (float)c_kvalues[b1 & 0xF]);
-      o[8 + j / 2] = g_bf16x2(dd * (float)c_kvalues[b0 >> 4], dd * (float)c_kvalues[b1 >> 4]);
-    }
-  }
-};
-
-template <> struct GDec<GQK_Q5_0> {
-  uint32_t qs[4], qh, d;
-  __device__ void load(const uint8_t* c, int r, int g) {
-    gld<16>(qs, col16(c, r, g)); gld<4>(&qh, col16(c + 64 * 128, r, g >> 2) + 4 * (g & 3)); gld<2>(&d, c + 64 * 160 + r * 16 + 2 * g);
-  }
-  __device__ void out(uint32_t* o) const {
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      uint32_t b0 = g_byte(qs, j), b1 = g_byte(qs, j + 1);
-      int l0 = (b0 & 0xF) | (((qh >> j) & 1) << 4), l1 = (b1 & 0xF) | (((qh >> (j + 1)) & 1) << 4);
-      int h0 = (b0 >> 4) | (((qh >> (j + 16)) & 1) << 4), h1 = (b1 >> 4) | (((qh >> (j + 17)) & 1) << 4);
-      o[j / 2] = g_bf16x2(dd * (float)(l0 - 16), dd * (float)(l1 - 16));
-      o[8 + j / 2] = g_bf16x2(dd * (float)(h0 - 16), dd * (float)(h1 - 16));
-    }
-  }
-};
-
-template <> struct GDec<GQK_Q8_0> {
-  uint32_t qs[8], d;
-  __device__ void load(const uint8_t* c, int r, int g) { gld<16>(qs, col16(c, r, 2 * g)); gld<16>(qs + 4, col16(c, r, 2 * g + 1)); gld<2>(&d, c + 64 * 256 + r * 16 + 2 * g); }
-  __device__ void out(uint32_t* o) const {
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int j = 0; j < 32; j += 2)
-      o[j / 2] = g_bf16x2(dd * (float)(int8_t)g_byte(qs, j), dd * (float)(int8_t)g_byte(qs, j + 1));
-  }
-};
-
-template <> struct GDec<GQK_Q2_K> {
-  uint32_t qs[8], sc, dd;
-  int t;
-  __device__ void load(const uint8_t* c, int r, int g) {
-    int h = g >> 2;
-    t = g & 3;
-    gld<16>(qs, col16(c, r, 2 * h));
-    gld<16>(qs + 4, col16(c, r, 2 * h + 1));
-    gld<2>(&sc, c + 64 * 64 + r * 16 + 2 * g);
-    gld<4>(&dd, c + 64 * 80 + r * 4);
-  }
-  __device__ void out(uint32_t* o) const {
-    float d = g_h2f(dd), dmin = g_h2f(dd >> 16);
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      uint32_t sb = (sc >> (8 * hf)) & 0xFF;
-      float dl = d * (float)(sb & 0xF), ml = dmin * (float)(sb >> 4);
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) {
-        int l = 16 * hf + j;
-        float w0 = dl * (float)((g_byte(qs, l) >> (2 * t)) & 3) - ml;
-        float w1 = dl * (float)((g_byte(qs, l + 1) >> (2 * t)) & 3) - ml;
-        o[l / 2] = g_bf16x2(w0, w1);
-      }
-    }
-  }
-};
-
-template <> struct GDec<GQK_Q3_K> {
-  uint32_t qs[8], hm[8], sb[3], d;
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    gld<16>(qs, col16(c, r, 2 * (g >> 2)));
-    gld<16>(qs + 4, col16(c, r, 2 * (g >> 2) + 1));
-    gld<16>(hm, col16(c + 64 * 64, r, 0));
-    gld<16>(hm + 4, col16(c + 64 * 64, r, 1));
-    const uint32_t* p = (const uint32_t*)(c + 64 * 96);   // three 4-byte columns
-    sb[0] = p[r]; sb[1] = p[64 + r]; sb[2] = p[128 + r];
-    gld<2>(&d, c + 64 * 108 + r * 2);
-  }
-  __device__ void out(uint32_t* o) const {
-    int n = g >> 2, jj = g & 3;
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      int i = 2 * g + hf;
-      int lo = (g_byte(sb, i % 8) >> (4 * (i / 8))) & 0xF;
-      int hi = (g_byte(sb, 8 + i % 4) >> (2 * (i / 4))) & 3;
-      float dl = dd * (float)((lo | (hi << 4)) - 32);
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) {
-        int l = 16 * hf + j;
-        int q0 = ((g_byte(qs, l) >> (2 * jj)) & 3) - (((g_byte(hm, l) >> (4 * n + jj)) & 1) ? 0 : 4);
-        int q1 = ((g_byte(qs, l + 1) >> (2 * jj)) & 3) - (((g_byte(hm, l + 1) >> (4 * n + jj)) & 1) ? 0 : 4);
-        o[l / 2] = g_bf16x2(dl * (float)q0, dl * (float)q1);
-      }
-    }
-  }
-};
-
-__device__ __forceinline__ void g_scale_min_k4(const uint32_t* S, int j, int& sc, int& m) {
-  if (j < 4) {
-    sc = g_byte(S, j) & 63;
-    m = g_byte(S, j + 4) & 63;
-  } else {
-    sc = (g_byte(S, j + 4) & 0xF) | ((g_byte(S, j - 4) >> 6) << 4);
-    m = (g_byte(S, j + 4) >> 4) | ((g_byte(S, j) >> 6) << 4);
-  }
-}
-
-template <> struct GDec<GQK_Q4_K> {
-  uint32_t qs[8], hdr[4];
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    gld<16>(qs, col16(c, r, 2 * (g >> 1)));
-    gld<16>(qs + 4, col16(c, r, 2 * (g >> 1) + 1));
-    gld<16>(hdr, c + 64 * 128 + r * 16);
-  }
-  __device__ void out(uint32_t* o) const {
-    int sc, m;
-    g_scale_min_k4(hdr + 1, g, sc, m);
-    float dl = g_h2f(hdr[0]) * (float)sc, ml = g_h2f(hdr[0] >> 16) * (float)m;
-    const int sh = 4 * (g & 1);
-#pragma unroll
-    for (int p = 0; p < 32; p += 2)
-      o[p / 2] = g_bf16x2(dl * (float)((g_byte(qs, p) >> sh) & 0xF) - ml, dl * (float)((g_byte(qs, p + 1) >> sh) & 0xF) - ml);
-  }
-};
-
-template <> struct GDec<GQK_Q5_K> {
-  uint32_t qs[8], qh[8], hdr[4];
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    gld<16>(qs, col16(c, r, 2 * (g >> 1)));
-    gld<16>(qs + 4, col16(c, r, 2 * (g >> 1) + 1));
-    gld<16>(qh, col16(c + 64 * 128, r, 0));
-    gld<16>(qh + 4, col16(c + 64 * 128, r, 1));
-    gld<16>(hdr, c + 64 * 160 + r * 16);
-  }
-  __device__ void out(uint32_t* o) const {
-    int sc, m;
-    g_scale_min_k4(hdr + 1, g, sc, m);
-    float dl = g_h2f(hdr[0]) * (float)sc, ml = g_h2f(hdr[0] >> 16) * (float)m;
-    const int sh = 4 * (g & 1);
-#pragma unroll
-    for (int p = 0; p < 32; p += 2) {
-      int q0 = ((g_byte(qs, p) >> sh) & 0xF) | (((g_byte(qh, p) >> g) & 1) << 4);
-      int q1 = ((g_byte(qs, p + 1) >> sh) & 0xF) | (((g_byte(qh, p + 1) >> g) & 1) << 4);
-      o[p / 2] = g_bf16x2(dl * (float)q0 - ml, dl * (float)q1 - ml);
-    }
-  }
-};
-
-template <> struct GDec<GQK_Q6_K> {
-  uint32_t ql[8], qh[8], sc, d;
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    int h = g >> 2, t = g & 3;
-    gld<16>(ql, col16(c, r, 4 * h + 2 * (t & 1)));
-    gld<16>(ql + 4, col16(c, r, 4 * h + 2 * (t & 1) + 1));
-    gld<16>(qh, col16(c + 64 * 128, r, 2 * h));
-    gld<16>(qh + 4, col16(c + 64 * 128, r, 2 * h + 1));
-    gld<2>(&sc, c + 64 * 192 + r * 16 + 2 * g);
-    gld<2>(&d, c + 64 * 208 + r * 2);
-  }
-  __device__ void out(uint32_t* o) const {
-    int t = g & 3;
-    float dd = g_h2f(d);
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      float dl = dd * (float)(int8_t)((sc >> (8 * hf)) & 0xFF);
-#pragma unroll
-      for (int j = 0; j < 16; j += 2) {
-        int p = 16 * hf + j;
-        int q0 = (((g_byte(ql, p) >> (4 * (t >> 1))) & 0xF) | (((g_byte(qh, p) >> (2 * t)) & 3) << 4)) - 32;
-        int q1 = (((g_byte(ql, p + 1) >> (4 * (t >> 1))) & 0xF) | (((g_byte(qh, p + 1) >> (2 * t)) & 3) << 4)) - 32;
-        o[p / 2] = g_bf16x2(dl * (float)q0, dl * (float)q1);
-      }
-    }
-  }
-};
-
-template <> struct GDec<GQK_IQ4_XS> {
-  uint32_t qs[4], hdr[2];
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    gld<16>(qs, col16(c, r, g));
-    gld<8>(hdr, c + 64 * 128 + r * 8);
-  }
-  __device__ void out(uint32_t* o) const {
-    int ls = ((hdr[1] >> (4 * g)) & 0xF) | (((hdr[0] >> (16 + 2 * g)) & 3) << 4);
-    float dl = g_h2f(hdr[0]) * (float)(ls - 32);
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      uint32_t b0 = g_byte(qs, j), b1 = g_byte(qs, j + 1);
-      o[j / 2] = g_bf16x2(dl * (float)c_kvalues[b0 & 0xF], dl * (float)c_kvalues[b1 & 0xF]);
-      o[8 + j / 2] = g_bf16x2(dl * (float)c_kvalues[b0 >> 4], dl * (float)c_kvalues[b1 >> 4]);
-    }
-  }
-};
-
-template <> struct GDec<GQK_IQ3_S> {
-  uint32_t qs[2], sg, qh[2], scb, d;
-  int g;
-  __device__ void load(const uint8_t* c, int r, int g_) {
-    g = g_;
-    gld<8>(qs, col16(c, r, g >> 1) + 8 * (g & 1));
-    gld<4>(&sg, col16(c + 64 * 64, r, g >> 2) + 4 * (g & 3));
-    gld<8>(qh, c + 64 * 96 + r * 8);
-    gld<4>(&scb, c + 64 * 104 + r * 4);
-    gld<2>(&d, c + 64 * 108 + r * 2);
-  }
-  __device__ void out(uint32_t* o) const {
-    float dl = g_h2f(d) * (float)(1 + 2 * (int)((scb >> (4 * g)) & 0xF));
-    uint32_t qhb = g_byte(qh, g);
-#pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      uint32_t sb = (sg >> (8 * l)) & 0xFF;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        uint32_t idx = g_byte(qs, 2 * l + half) | ((qhb << (8 - 2 * l - half)) & 256);
-        uint32_t gw = c_iq3s_grid[idx];
-        float v[4];
-#pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) {
-          float a = dl * (float)((gw >> (8 * k4)) & 0xFF);
-          v[k4] = ((sb >> (4 * half + k4)) & 1) ? -a : a;
-        }
-        o[4 * l + 2 * half] = g_bf16x2(v[0], v[1]);
-        o[4 * l + 2 * half + 1] = g_bf16x2(v[2], v[3]);
-      }
-    }
-  }
-};
-
-#define GEMM_BN 128
-#define GEMM_BK 64
-#define GEMM_LDK (GEMM_BK + 8)   // LDS row stride in bf16 (16 B pad)
-
-template <int BM, int T>
-__device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
-                                          const uint16_t* __restrict__ x, int64_t ldx, int M, uint16_t* __restrict__ y,
-                                          int64_t ldy, uint16_t* As, uint16_t* Bs) {
-  constexpr int WM = BM / 2;              // tokens per wave (2 x 2 waves)
-  constexpr int MB = WM / 32;             // 32-token MFMA blocks per wave
-  constexpr int AV = BM * GEMM_BK / 8 / 256;   // uint4 of x per thread per step
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int nb = dsc[D_NB];
-  const int ntiles = dsc[D_NTILES];
-  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
-  const int64_t tile0 = dsc[D_TILE0];
-  const int m0 = blockIdx.y * BM;
-  constexpr int REC = gqk_layout<T>::REC;
-
-  // B-decode role: thread -> (weight row br = tid / 2 in the 128-row block, 32-weight half bh)
-  const int br = tid >> 1, bh = tid & 1;
-  const int btile = br >> 6, brow = br & 63;
-  const bool bvalid = btile < ntiles;
-  const uint8_t* bbase = packed + off + (tile0 + (bvalid ? btile : 0)) * nb * (int64_t)(64 * REC);
-
-  v16f acc[MB][2];
-#pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nsteps = nb * 4;
-  uint4 areg[AV];
-  GDec<T> breg;
-
-  auto gload = [&](int step) {
-    const int kb = step >> 2, kq = step & 3;
-#pragma unroll
-    for (int a = 0; a < AV; ++a) {
-      int e = tid + 256 * a;          // uint4 index in the BM x 64 tile: row e / 8, col 8 * (e % 8)
-      int row = e >> 3, c8 = e & 7;
-      int t = m0 + row;
-      areg[a] = t < M ? *(const uint4*)(x + (int64_t)t * ldx + (int64_t)step * GEMM_BK + 8 * c8) : make_uint4(0, 0, 0, 0);
-    }
-    breg.load(bbase + (int64_t)kb * 64 * REC, brow, 2 * kq + bh);
-  };
-  auto lstore = [&](int buf) {
-    uint16_t* as = As + buf * BM * GEMM_LDK;
-    uint16_t* bs = Bs + buf * GEMM_BN * GEMM_LDK;
-#pragma unroll
-    for (int a = 0; a < AV; ++a) {
-      int e = tid + 256 * a;
-      int row = e >> 3, c8 = e & 7;
-      *(uint4*)(as + row * GEMM_LDK + 8 * c8) = areg[a];
-    }
-    uint32_t o[16];
-    if (bvalid) breg.out(o);
-    else
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[i] = 0;
-    uint4* dst = (uint4*)(bs + br * GEMM_LDK + 32 * bh);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-  };
-
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    if (step + 1 < nsteps) gload(step + 1);
-    const uint16_t* as = As + buf * BM * GEMM_LDK;
-    const uint16_t* bs = Bs + buf * GEMM_BN * GEMM_LDK;
-#pragma unroll
-    for (int kk = 0; kk < GEMM_BK; kk += 16) {
-      const int kl = kk + 8 * (lane >> 5);
-      v8bf bf[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *(const v8bf*)(bs + (wn * 64 + 32 * j + (lane & 31)) * GEMM_LDK + kl);
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        v8bf af = *(const v8bf*)(as + (wm * WM + 32 * i + (lane & 31)) * GEMM_LDK + kl);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[j], acc[i][j], 0, 0, 0);
-      }
-    }
-    if (step + 1 < nsteps) lstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // C block (i, j): lane -> weight row 32 j + (lane & 31), tokens 8 (v / 4) + 4 (lane / 32) + v % 4
-  const int nvalid = dsc[D_NVALID];
-  const int64_t col0 = dsc[D_COL0];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = wn * 64 + 32 * j + (lane & 31);
-    if (r >= nvalid) continue;
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int t = m0 + wm * WM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (t < M) y[(int64_t)t * ldy + col0 + r] = __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][v]);
-      }
-  }
-}
-
-template <int BM, int ONLY>
-__global__ __launch_bounds__(256) void gemm_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
-                                                   const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                   uint16_t* __restrict__ y, int64_t ldy) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2 * BM * GEMM_LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2 * GEMM_BN * GEMM_LDK];
-  const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
-  const int type = dsc[D_TYPE];
-#define RUN(T) if ((ONLY == 0 || ONLY == T) && type == T) gemm_tile<BM, T>(packed, dsc, x, ldx, M, y, ldy, As, Bs);
-  RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
-  RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
-#undef RUN
-}
-
-// ---- the 256 x 256 form (M > 128) ------------------------------------------------------------
-// Workgroup = 512 threads (8 waves, two per SIMD): 256 tokens x 256 weight rows (four tiles of one
-// shard), K in steps of 64.  Wave (wm, wn) owns tokens 64 wm .. +63 and rows 128 wn .. +127 (2 x 4
-// blocks of v_mfma_f32_32x32x16_bf16).  Per step each thread decodes 32 weights of one row (two
-// runs of 16 at step-local offsets OFF0 / OFF1, per type) and stages 32 activations of one token;
-// the next step's loads are in flight during the MFMAs.  LDS: x and weights double-buffered
-// (147,456 bytes) plus the IQ3_S tables, one workgroup per CU.
-
-#define GB_M 256
-#define GB_N 256
 #define GQK_GB_WORD3 0x00020000   // buffer resource word 3: raw untyped dword access
 #define GQK_GB_SC1 16             // device-scope cache policy (write through / bypass the XCD L2)
 #define GB_K 64
@@ -719,48 +332,65 @@ template <> struct B2<GQK_IQ3_S> {   // group g = 2 kq + h: 32 weights, magnitud
   }
 };
 
-// LDS bytes of the 256 form: x and weight tiles, double-buffered, then the IQ3_S tables
-#define GB_TILE_BYTES (2 * (GB_M + GB_N) * GB_LD * 2)
+// LDS bytes of the IQ3_S tables (after the tiles)
 #define GB_TAB_BYTES (512 * 4 + 256 * 16)
 
 // Where a tile's accumulators go: straight to y (part == nullptr), or - for a tile whose k-steps
 // are shared by several workgroups (stream-K) - to this workgroup's fp32 partial slot, the last
 // contributor to arrive summing every slot in k order (deterministic) and writing y.
 struct GOut {
-  float* part;   // partial slots, 256 x 256 fp32 each
+  float* part;   // partial slots, BM x BN fp32 each
   int* ctr;      // the tile's arrival counter (zero at rest, reset by the last contributor)
   int slot0;     // slot of the tile's first contributor
   int nc;        // contributors
   int self;      // this workgroup's index among them
 };
 
-#define GB_SLOT_FLOATS (GB_M * GB_N)
+// Tile geometry: BM tokens x BN weight rows per tile, a WGM x WGN grid of waves each owning
+// (BM / WGM) x (BN / WGN) outputs in 32 x 32 MFMA blocks.  Thread t decodes part t & 1 of weight
+// row t >> 1 each step, and stages AV 16-byte chunks of x.
+template <int BM_, int BN_, int WGM_, int WGN_>
+struct Geo {
+  static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NW = WGM * WGN, NT = 64 * NW;
+  static constexpr int MB = BM / WGM / 32, NB = BN / WGN / 32;   // 32 x 32 blocks per wave
+  static constexpr int AV = BM * 8 / NT;                          // x chunks per thread per step
+  static constexpr int CH = MB * NB * 4;                          // 16-byte accumulator chunks per thread
+  static constexpr int SLOT = BM * BN;                            // floats per partial slot
+  static constexpr int LDS = 2 * (BM + BN) * GB_LD * 2;           // double-buffered x and weights
+  static_assert(BN * 2 == NT, "one thread per (weight row, part)");
+  static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
+};
+typedef Geo<256, 256, 4, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
+typedef Geo<128, 128, 2, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
+typedef Geo<64, 128, 2, 2> GeoSmall;   // 33..64 tokens
 
-template <int T>
-__device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
-                                              const uint16_t* __restrict__ x, int64_t ldx, int M, int m0, int k0,
-                                              int k1, const GOut& go, uint16_t* __restrict__ y, int64_t ldy,
-                                              uint16_t* As, uint16_t* Bs, int* flag, const GTabs& tb) {
+template <class GE, int T>
+__device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
+                                             const uint16_t* __restrict__ x, int64_t ldx, int M, int m0, int k0,
+                                             int k1, const GOut& go, uint16_t* __restrict__ y, int64_t ldy,
+                                             uint16_t* As, uint16_t* Bs, int* flag, const GTabs& tb) {
   constexpr int REC = gqk_layout<T>::REC;
+  constexpr int MB = GE::MB, NB = GE::NB, AV = GE::AV, NT = GE::NT;
+  constexpr int WTM = GE::BM / GE::WGM, WTN = GE::BN / GE::WGN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 3, wn = wave >> 2;
+  const int wm = wave % GE::WGM, wn = wave / GE::WGM;
   const int nb = dsc[D_NB], ntiles = dsc[D_NTILES];
   const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
   const int64_t tile0 = dsc[D_TILE0];
 
-  // weight role: row br of the 256-row block, part h of the step's 64 weights
+  // weight role: row br of the tile's BN rows, part h of the step's 64 weights
   const int br = tid >> 1, h = tid & 1;
   const int btile = br >> 6, brow = br & 63;
   const uint8_t* bbase = packed + off + (tile0 + (btile < ntiles ? btile : 0)) * nb * (int64_t)(64 * REC);
-  // activation role: token ar of the block, 32 of the step's 64 k
-  const int ar = tid >> 1, ah = tid & 1;
-  const uint16_t* abase = x + (int64_t)min(m0 + ar, M - 1) * ldx + 32 * ah;
+  // activation role: AV consecutive 16-byte chunks (8 k each) of token ar
+  const int ar = tid * AV / 8, ac = (tid * AV) % 8;
+  const uint16_t* abase = x + (int64_t)min(m0 + ar, M - 1) * ldx + 8 * ac;
 
-  v16f acc[2][4];
+  v16f acc[MB][NB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
@@ -771,22 +401,22 @@ __device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed
   // (clamped to the last step).  Rows past M (x) and past the shard's rows (weights) hold clamped
   // copies of real data: they only reach accumulator entries that are never stored.
   const int last = k1 - 1;
-  uint4 av[4];
+  uint4 av[AV];
   B2<T> p0, p1;
   auto xload = [&](int s) {
     const uint4* ap = (const uint4*)(abase + (int64_t)s * GB_K);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) av[i] = ap[i];
+    for (int i = 0; i < AV; ++i) av[i] = ap[i];
   };
   auto xstore = [&](int buf) {
-    uint4* as = (uint4*)(As + (buf * GB_M + ar) * GB_LD + 32 * ah);
+    uint4* as = (uint4*)(As + (buf * GE::BM + ar) * GB_LD + 8 * ac);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) as[i] = av[i];
+    for (int i = 0; i < AV; ++i) as[i] = av[i];
   };
   auto wload = [&](B2<T>& p, int s) { p.load(bbase + (int64_t)(s >> 2) * (64 * REC), brow, s & 3, h); };
   auto wdecode = [&](const B2<T>& p, int s, uint32_t (&o)[16], int i) { p.out(s & 3, h, o, tb, i); };
   auto wstore = [&](const uint32_t (&o)[16], int buf) {
-    uint16_t* bs = Bs + (buf * GB_N + br) * GB_LD;
+    uint16_t* bs = Bs + (buf * GE::BN + br) * GB_LD;
     uint4* d0 = (uint4*)(bs + B2<T>::off0(h));
     uint4* d1 = (uint4*)(bs + B2<T>::off1(h));
     d0[0] = make_uint4(o[0], o[1], o[2], o[3]);
@@ -798,20 +428,20 @@ __device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed
     const int buf = (s - k0) & 1;
     xload(min(s + 1, last));
     wload(pl, min(s + 2, last));
-    const uint16_t* as = As + (buf * GB_M + wm * 64 + (lane & 31)) * GB_LD + 8 * (lane >> 5);
-    const uint16_t* bs = Bs + (buf * GB_N + wn * 128 + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    const uint16_t* as = As + (buf * GE::BM + wm * WTM + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    const uint16_t* bs = Bs + (buf * GE::BN + wn * WTN + (lane & 31)) * GB_LD + 8 * (lane >> 5);
     uint32_t o[16];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      v8bf af[2], bf[4];
+      v8bf af[MB], bf[NB];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *(const v8bf*)(as + 32 * i * GB_LD + 16 * kk);
+      for (int i = 0; i < MB; ++i) af[i] = *(const v8bf*)(as + 32 * i * GB_LD + 16 * kk);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = *(const v8bf*)(bs + 32 * j * GB_LD + 16 * kk);
+      for (int j = 0; j < NB; ++j) bf[j] = *(const v8bf*)(bs + 32 * j * GB_LD + 16 * kk);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
       wdecode(pd, s + 1, o, kk);
     }
     xstore(buf ^ 1);
@@ -841,31 +471,30 @@ __device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed
   const int nvalid = dsc[D_NVALID];
   const int64_t col0 = dsc[D_COL0];
   auto store_y = [&](int i, int j, const v16f& a) {
-    const int r = wn * 128 + 32 * j + (lane & 31);
+    const int r = wn * WTN + 32 * j + (lane & 31);
     if (r >= nvalid) return;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int t = m0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      const int t = m0 + wm * WTM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
       if (t < M) y[(int64_t)t * ldy + col0 + r] = __builtin_bit_cast(uint16_t, (__bf16)a[v]);
     }
   };
   if (go.part == nullptr) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) store_y(i, j, acc[i][j]);
+      for (int j = 0; j < NB; ++j) store_y(i, j, acc[i][j]);
     return;
   }
-  // Partial slot layout: chunk c (16 bytes: elements 4 (c & 3) .. of acc[c >> 4][(c >> 2) & 3]) of
-  // thread tid at ((slot * 32 + c) * 512 + tid) * 16, so every store and load is coalesced.
-  const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(go.part + (int64_t)go.slot0 * GB_SLOT_FLOATS, 0, go.nc * GB_SLOT_FLOATS * 4,
-                                        GQK_GB_WORD3);
+  // Partial slot layout: chunk c (elements 4 (c & 3) .. of acc[c / (4 NB)][(c / 4) % NB]) of thread
+  // tid at ((slot * CH + c) * NT + tid) * 16, so every store and load is coalesced.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      go.part + (int64_t)go.slot0 * GE::SLOT, 0, go.nc * GE::SLOT * 4, GQK_GB_WORD3);
 #pragma unroll
-  for (int c = 0; c < 32; ++c) {
-    const v16f& a = acc[c >> 4][(c >> 2) & 3];
+  for (int c = 0; c < GE::CH; ++c) {
+    const v16f& a = acc[c / (4 * NB)][(c / 4) % NB];
     const v4f q = {a[4 * (c & 3)], a[4 * (c & 3) + 1], a[4 * (c & 3) + 2], a[4 * (c & 3) + 3]};
-    __builtin_amdgcn_raw_buffer_store_b128(q, rs, ((go.self * 32 + c) * 512 + tid) * 16, 0, GQK_GB_SC1);
+    __builtin_amdgcn_raw_buffer_store_b128(q, rs, ((go.self * GE::CH + c) * NT + tid) * 16, 0, GQK_GB_SC1);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this workgroup's partial is complete
   __syncthreads();
@@ -873,20 +502,20 @@ __device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed
   __syncthreads();
   if (*flag != go.nc - 1) return;
   asm volatile("" ::: "memory");
-  // the last contributor: slot 0 + slot 1 + ... in k order, one 32 x 32 block (acc[i][j]) at a time
+  // the last contributor: slot 0 + slot 1 + ... in k order, one 32 x 32 block at a time
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c0 = 16 * i + 4 * j;
+    for (int j = 0; j < NB; ++j) {
+      const int c0 = (i * NB + j) * 4;
       v4f sum[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sum[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((c0 + e) * 512 + tid) * 16, 0, GQK_GB_SC1);
+      for (int e = 0; e < 4; ++e) sum[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((c0 + e) * NT + tid) * 16, 0, GQK_GB_SC1);
       for (int q = 1; q < go.nc; ++q) {
         v4f t[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          t[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((q * 32 + c0 + e) * 512 + tid) * 16, 0, GQK_GB_SC1);
+          t[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((q * GE::CH + c0 + e) * NT + tid) * 16, 0, GQK_GB_SC1);
 #pragma unroll
         for (int e = 0; e < 4; ++e) sum[e] += t[e];
       }
@@ -897,10 +526,10 @@ __device__ __forceinline__ void gemm_big_tile(const uint8_t* __restrict__ packed
   if (tid == 0) __hip_atomic_store(go.ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
-// Tile t -> (descriptor row, 256-token block).  Groups of up to eight token blocks take
-// consecutive tile ids, so with tiles dealt round robin to the workgroups and the dispatcher's
-// round robin over the eight XCDs, each XCD keeps one token block (256 x K activations) hot in
-// its L2 while the weight blocks stream by.
+// Tile t -> (descriptor row, token block).  Groups of up to eight token blocks take consecutive
+// tile ids, so with tiles dealt round robin to the workgroups and the dispatcher's round robin
+// over the eight XCDs, each XCD keeps one token block of x hot in its L2 while the weight blocks
+// stream by.
 __device__ __forceinline__ void gb_map(int i, int n_desc, int nmb, int& d, int& mb) {
   const int full = (nmb / 8) * 8 * n_desc;
   if (i < full) {
@@ -914,32 +543,32 @@ __device__ __forceinline__ void gb_map(int i, int n_desc, int nmb, int& d, int& 
   }
 }
 
-// Persistent schedule over G workgroups (one per CU): the first floor(T / G) * G tiles whole,
+// Persistent schedule over G workgroups (all resident: two waves per SIMD, so at most 256 registers
+// a lane; no workgroup ever waits for another, so residency is a matter of speed only): the first floor(T / G) * G tiles whole,
 // dealt round robin; the remaining R tiles' k-steps split evenly over G_sk = min(G, R * steps)
 // workgroups (stream-K), tiles shared by several workgroups combined through partial slots.
-template <int ONLY>
-__global__ __launch_bounds__(512) void gemm_big_kernel(const uint8_t* __restrict__ packed,
-                                                       const int32_t* __restrict__ desc, int n_desc,
-                                                       const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                       uint16_t* __restrict__ y, int64_t ldy, float* part, int* ctr,
-                                                       int G) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[GB_TILE_BYTES + GB_TAB_BYTES + 16];
+template <class GE, int ONLY>
+__global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_sk_kernel(const uint8_t* __restrict__ packed,
+                                                          const int32_t* __restrict__ desc, int n_desc,
+                                                          const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                          uint16_t* __restrict__ y, int64_t ldy, float* part, int* ctr,
+                                                          int G) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[GE::LDS + GB_TAB_BYTES + 16];
   uint16_t* As = (uint16_t*)lds;
-  uint16_t* Bs = As + 2 * GB_M * GB_LD;
-  int* flag = (int*)(lds + GB_TILE_BYTES + GB_TAB_BYTES);
+  uint16_t* Bs = As + 2 * GE::BM * GB_LD;
+  int* flag = (int*)(lds + GE::LDS + GB_TAB_BYTES);
   GTabs tb;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     tb.kv[i] = (uint32_t)(c_kvalues[4 * i] + 128) | ((uint32_t)(c_kvalues[4 * i + 1] + 128) << 8) |
                ((uint32_t)(c_kvalues[4 * i + 2] + 128) << 16) | ((uint32_t)(c_kvalues[4 * i + 3] + 128) << 24);
-  uint32_t* grid = (uint32_t*)(lds + GB_TILE_BYTES);
-  uint4* sign = (uint4*)(lds + GB_TILE_BYTES + 512 * 4);
+  uint32_t* grid = (uint32_t*)(lds + GE::LDS);
+  uint4* sign = (uint4*)(lds + GE::LDS + 512 * 4);
   tb.grid = grid;
   tb.sign = sign;
   if (ONLY == 0 || ONLY == GQK_IQ3_S) {
-    const int t = threadIdx.x;
-    grid[t] = c_iq3s_grid[t];
-    if (t < 256) {
+    for (int t = threadIdx.x; t < 512; t += GE::NT) grid[t] = c_iq3s_grid[t];
+    for (int t = threadIdx.x; t < 256; t += GE::NT) {
       uint32_t m[4];
 #pragma unroll
       for (int p = 0; p < 4; ++p) m[p] = (((t >> (2 * p)) & 1) << 15) | (((t >> (2 * p + 1)) & 1) << 31);
@@ -947,7 +576,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(const uint8_t* __restrict
     }
     __syncthreads();
   }
-  const int nmb = (M + GB_M - 1) / GB_M;
+  const int nmb = (M + GE::BM - 1) / GE::BM;
   const int T = n_desc * nmb;
   const int nsteps = 4 * desc[D_NB];
   auto run = [&](int t, int k0, int k1, const GOut& go) {
@@ -957,7 +586,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(const uint8_t* __restrict
     const int type = dsc[D_TYPE];
 #define RUN(TY)                                                                                          \
     if ((ONLY == 0 || ONLY == TY) && type == TY)                                                         \
-      gemm_big_tile<TY>(packed, dsc, x, ldx, M, mb * GB_M, k0, k1, go, y, ldy, As, Bs, flag, tb);
+      gemm_tile_sk<GE, TY>(packed, dsc, x, ldx, M, mb * GE::BM, k0, k1, go, y, ldy, As, Bs, flag, tb);
     RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
     RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
@@ -999,7 +628,7 @@ __global__ __launch_bounds__(512) void gemm_big_kernel(const uint8_t* __restrict
   }
 }
 
-// CUs of the current device (one 256 x 256 workgroup fits per CU), cached per device
+// CUs of the current device, cached per device
 static int gb_cus() {
   static int cache[64] = {0};
   int dev = 0;
@@ -1012,65 +641,55 @@ static int gb_cus() {
   return cache[dev];
 }
 
-int64_t gemm_big_workspace(int n_desc, int M, int nb) {
-  const int G = gb_cus();
+// persistent workgroups of a form: every one resident (the 256 form takes a whole CU's LDS)
+static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : 2); }
+static int gb_slot_floats(int bm) { return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : GeoSmall::SLOT; }
+
+int64_t gemm_workspace(int bm, int n_desc, int M, int nb) {
+  const int G = gb_workgroups(bm);
   if (G <= 0) return -1;
-  const int64_t T = (int64_t)n_desc * ((M + GB_M - 1) / GB_M);
+  const int64_t T = (int64_t)n_desc * ((M + bm - 1) / bm);
   const int64_t R = T % G;
   if (R == 0) return 0;
   const int64_t gsk = std::min<int64_t>(G, R * 4 * nb);
-  return (G * 4 + 255) / 256 * 256 + (R + gsk - 1) * GB_SLOT_FLOATS * 4;
+  return ((int64_t)G * 4 + 255) / 256 * 256 + (R + gsk - 1) * gb_slot_floats(bm) * 4;
 }
 
-static int launch_big(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
-                      const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, void* ws, int64_t ws_bytes) {
-  const int G = gb_cus();
+template <class GE>
+static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
+                     const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, void* ws, int64_t ws_bytes) {
+  const int G = gb_workgroups(GE::BM);
   if (G <= 0) return GQK_ERR_HIP;
-  const int64_t need = gemm_big_workspace(n_desc, M, nb);
+  const int64_t need = gemm_workspace(GE::BM, n_desc, M, nb);
   if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255))) return GQK_ERR_SHAPE;
   int* ctr = (int*)ws;
-  float* part = need > 0 ? (float*)((char*)ws + (G * 4 + 255) / 256 * 256) : nullptr;
+  float* part = need > 0 ? (float*)((char*)ws + ((int64_t)G * 4 + 255) / 256 * 256) : nullptr;
   // G workgroups when there are at least G tiles; else every stream-K participant,
   // min(G, T * steps) (the kernel splits the steps of all T tiles over that many)
-  const int64_t T = (int64_t)n_desc * ((M + GB_M - 1) / GB_M);
+  const int64_t T = (int64_t)n_desc * ((M + GE::BM - 1) / GE::BM);
   dim3 grid((unsigned)(T >= G ? G : std::min<int64_t>(G, T * 4 * nb)));
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemm_big_kernel<T>), grid, dim3(512), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G); return GQK_OK;
+#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G); return GQK_OK;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemm_big_kernel<0>), grid, dim3(512), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G);
+      hipLaunchKernelGGL((gemm_sk_kernel<GE, 0>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G);
   }
   return GQK_OK;
-}
-
-template <int BM>
-static void launch_bm(int only, dim3 grid, hipStream_t st, const uint8_t* packed, const int32_t* desc, const uint16_t* x,
-                      int64_t ldx, int M, uint16_t* y, int64_t ldy) {
-  switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemm_kernel<BM, T>), grid, dim3(256), 0, st, packed, desc, x, ldx, M, y, ldy); return;
-    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
-    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
-#undef C
-    default:
-      hipLaunchKernelGGL((gemm_kernel<BM, 0>), grid, dim3(256), 0, st, packed, desc, x, ldx, M, y, ldy);
-  }
 }
 
 int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
                 int M, int64_t K, void* y, int64_t ldy, int bm, void* ws, int64_t ws_bytes, hipStream_t st) {
-  dim3 grid(n_desc, (M + bm - 1) / bm);
-  if (bm == 256)
-    return launch_big(types_mask, n_desc, M, (int)(K / 256), st, packed, desc, (const uint16_t*)x, ldx, (uint16_t*)y, ldy,
-                      ws, ws_bytes);
-  else if (bm == 128)
-    launch_bm<128>(types_mask, grid, st, packed, desc, (const uint16_t*)x, ldx, M, (uint16_t*)y, ldy);
-  else if (bm == 64)
-    launch_bm<64>(types_mask, grid, st, packed, desc, (const uint16_t*)x, ldx, M, (uint16_t*)y, ldy);
-  else
-    return GQK_ERR_FORM;
-  return GQK_OK;
+  const int nb = (int)(K / 256);
+  const uint16_t* xx = (const uint16_t*)x;
+  uint16_t* yy = (uint16_t*)y;
+  switch (bm) {
+    case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
+    case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
+    case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
+    default: return GQK_ERR_FORM;
+  }
 }
 
 }  // namespace gqk

@@ -1,13 +1,13 @@
-// gqk_gemv.hip - the grouped decode GEMV (batch rows M <= 32) over mixed-type tile shards.
+// gqk_gemv.hip - the grouped decode GEMV (batch rows M <= 16) over mixed-type tile shards.
 //
 // Replaces the reference's grouped Gluon kernel for decode (tiles_grouped_kernel / _run /
 // grouped_gemm, gguf-plugin/gluon/tiles_grouped.py:304-1275, dispatched for M <= 32 by
 // gluon_mul_mat_tiles_grouped, gguf-plugin/gluon/interface.py:169-182), with bf16 activations
-// in place of its int8 ones.
+// in place of its int8 ones.  Here it serves M <= 16; the GEMM form is faster from 17 rows.
 //
-// Work split.  One workgroup (4 waves) per descriptor row: the row names a shard, one 64-row
-// tile of it and a k-range of 256-weight super-blocks, which the four waves split into
-// quarters.  The type is uniform per workgroup.  Lane r of a wave owns weight row r of the tile
+// Work split.  One workgroup (nw waves, chosen by the planner) per descriptor row: the row names
+// a shard, one 64-row tile of it and a k-range of 256-weight super-blocks, which the waves split
+// evenly.  The type is uniform per workgroup.  Lane r of a wave owns weight row r of the tile
 // and streams that row's record planes with 16-byte loads (one coalesced 1 KiB access per plane
 // column); each wave stages its own slice of x in a private LDS region, so the main loop has no
 // workgroup barrier.
@@ -601,7 +601,7 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   if (arrived != split - 1) return;
   asm volatile("" ::: "memory");
   // the last workgroup: every partial of the tile, QC splits per round trip, summed in split order
-  constexpr int QC = G <= 2 ? 8 : (G == 4 ? 4 : 2);
+  constexpr int QC = G <= 2 ? 8 : 4;
   v4f a[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) a[g] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -651,7 +651,7 @@ static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t*
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
                 int M, int G, int nw, void* y, int64_t ldy, float* partials, int* counters, int split, int64_t n_total,
                 hipStream_t st) {
-  if (nw < 1 || nw > GQK_GEMV_MAX_WAVES || (G == 8 && 2 * nw > GQK_GEMV_MAX_WAVES)) return GQK_ERR_FORM;
+  if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
   dim3 grid(n_desc);
   float* part = split > 1 ? partials : nullptr;
   const uint16_t* xx = (const uint16_t*)x;
@@ -660,7 +660,6 @@ int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int type
     case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
     case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
     case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 8: launch_g<8>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
     default: return GQK_ERR_FORM;
   }
   return GQK_OK;

@@ -28,8 +28,8 @@ extern "C" {
 #define GQK_ERR_HIP (-4)   /* HIP runtime error at launch */
 #define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
 
-#define GQK_FORM_GEMV 1 /* M <= 32: in-register decode GEMV (MFMA 4x4x4 per scale group) */
-#define GQK_FORM_GEMM 2 /* M > 32: LDS-dequant bf16 MFMA GEMM */
+#define GQK_FORM_GEMV 1 /* M <= 16: in-register decode GEMV (MFMA 4x4x4 per scale group) */
+#define GQK_FORM_GEMM 2 /* M > 16: LDS-dequant bf16 MFMA GEMM */
 
 #define GQK_DTYPE_F32 0
 #define GQK_DTYPE_BF16 1
@@ -47,8 +47,8 @@ typedef struct gqk_shard {
 typedef struct gqk_plan_info {
   int32_t form;       /* GQK_FORM_GEMV or GQK_FORM_GEMM */
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
-  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4, 8) */
-  int32_t bm;         /* GEMM: tokens per workgroup (64, 128) */
+  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4) */
+  int32_t bm;         /* GEMM: tokens per tile (64, 128, 256) */
   int32_t split;      /* GEMV: split-K factor (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */

@@ -126,11 +126,11 @@ def test_plan_descriptor_rows_mixed_layer():
 def test_plan_buckets():
     from gguf_hip import ops
 
-    for M, g in ((1, 1), (4, 1), (5, 2), (8, 2), (9, 4), (16, 4), (17, 8), (32, 8)):
+    for M, g in ((1, 1), (4, 1), (5, 2), (8, 2), (9, 4), (16, 4)):
         info, _ = ops.plan([(12, 512, 0)], 512, M)
         assert info.form == 1 and info.g == g and info.m_max == 4 * g
-    assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 32) == 3
-    assert ops._pick_plan([], 33) == 4 and ops._pick_plan([], 64) == 4 and ops._pick_plan([], 65) == 5
-    assert ops._pick_plan([], 128) == 5 and ops._pick_plan([], 129) == 6 and ops._pick_plan([], 8192) == 6
-    for M, bm in ((33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
+    assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 16) == 2
+    assert ops._pick_plan([], 17) == 3 and ops._pick_plan([], 64) == 3 and ops._pick_plan([], 65) == 4
+    assert ops._pick_plan([], 128) == 4 and ops._pick_plan([], 129) == 5 and ops._pick_plan([], 8192) == 5
+    for M, bm in ((17, 64), (32, 64), (33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
         assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm

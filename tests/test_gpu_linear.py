@@ -1,4 +1,4 @@
-"""GPU parity of the grouped linear op (GEMV form M <= 32, GEMM form M > 32) against the
+"""GPU parity of the grouped linear op (GEMV form M <= 16, GEMM form M > 16) against the
 oracle: y = x @ dequant(W)^T in fp64 on the oracle's weights, tolerance 1e-2 relative to each
 output row's max |y| (metric of gguf-plugin/test_gluon_kq_gpu.py:81-86).
 Also: determinism, mixed-type layers, the GGUFLinearMethod surface, BASELINE config 1."""
@@ -202,11 +202,14 @@ def test_baseline_config1_q8_0(dev):
     assert e < TOL, e
 
 
-@pytest.mark.parametrize("n,K,M", [(1000, 2048, 300), (1000, 2048, 2148), (16384, 512, 1100)], ids=str)
+@pytest.mark.parametrize("n,K,M", [(1000, 2048, 300), (1000, 2048, 2148), (16384, 512, 1100),
+                                   (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120)],
+                         ids=str)
 def test_gemm_stream_k_schedule(dev, n, K, M):
-    """The 256 x 256 GEMM's persistent schedule: whole tiles dealt to the CUs, the remainder
-    tiles' k-steps split over all of them (stream-K) and combined in k order by the last
-    contributor.  Small grids are all remainder, the 16384-row case mixes both phases.  Checked
+    """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows, 128 x 128 and 64 x 128
+    at 65..128 and 33..64): whole tiles dealt to the workgroups, the remainder tiles' k-steps split
+    over all of them (stream-K) and combined in k order by the last contributor.  Small grids are
+    all remainder; the 16384-row case at M=1100 and the 70000-row cases mix both phases.  Checked
     against an fp32 matmul of the GPU-dequantized weights (pinned bit-exact by the dequant
     tests), repeated launches bit-identical, counters back at zero."""
     import gguf_hip
