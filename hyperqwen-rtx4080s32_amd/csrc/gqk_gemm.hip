@@ -10,6 +10,8 @@
 // along K (stream-K) and their partial sums combined in a fixed order.
 #include <hip/hip_runtime.h>
 #include <algorithm>
+#include <numeric>
+#include <type_traits>
 #include "gqk_common.h"
 #include "gqk_internal.h"
 
@@ -18,6 +20,7 @@ namespace gqk {
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float g_h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFF));
@@ -75,8 +78,18 @@ struct GTabs {
   const uint4* sign;       // IQ3_S sign masks of a sign byte: bits 15 / 31 of four bf16 pairs (LDS)
 };
 
-// fma(dl, u_i, bias) for the four unsigned bytes u_i of u -> two bf16 pairs (RNE)
+// Per-step constants of a decoder (scales and biases of the step's two scale groups, or one),
+// computed once per step by prep() and used by each quarter of out().
+struct GS {
+  float dl0, b0, dl1, b1;
+  uint32_t aux;
+};
+
+// fma(dl, u_i, bias) for the four unsigned bytes u_i of u -> two bf16 pairs (RNE).  The empty asm
+// hides u's known zero bits, so each byte converts with one v_cvt_f32_ubyteN instead of a
+// bit-field extract plus a conversion.
 __device__ __forceinline__ void cvt4(uint32_t u, float dl, float bias, uint32_t* o) {
+  asm("" : "+v"(u));
   o[0] = g_bf16x2(__builtin_fmaf(dl, (float)(u & 0xFF), bias), __builtin_fmaf(dl, (float)((u >> 8) & 0xFF), bias));
   o[1] = g_bf16x2(__builtin_fmaf(dl, (float)((u >> 16) & 0xFF), bias), __builtin_fmaf(dl, (float)(u >> 24), bias));
 }
@@ -100,6 +113,14 @@ __device__ __forceinline__ void k4_scale(const uint32_t* hdr, int j, int& sc, in
     m = (int)((b >> 4) | (((s01 >> (8 * j)) & 0xC0) >> 2));
   }
 }
+// Q4_K / Q5_K constants of step kq: sub-blocks 2 kq (dl0, b0) and 2 kq + 1 (dl1, b1)
+__device__ __forceinline__ GS k4_prep(const uint32_t* hdr, int kq) {
+  int sc0, m0, sc1, m1;
+  k4_scale(hdr, 2 * kq, sc0, m0);
+  k4_scale(hdr, 2 * kq + 1, sc1, m1);
+  const float d = g_h2f(hdr[0]), dm = g_h2f(hdr[0] >> 16);
+  return GS{d * (float)sc0, -(dm * (float)m0), d * (float)sc1, -(dm * (float)m1), 0};
+}
 // Q3_K signed 6-bit scale i (0..15) from the 12 packed bytes
 __device__ __forceinline__ int q3_scale(const uint32_t* sb, int i) {
   const uint64_t s01 = (uint64_t)sb[0] | ((uint64_t)sb[1] << 32);
@@ -117,12 +138,13 @@ template <> struct B2<GQK_Q4_0> {   // block b = 2 kq + h: low nibbles -> 16 wei
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * kq + h)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * (2 * kq + h));
   }
-  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int, int) const {
     const float dd = g_h2f(d);
-    {
-      cvt4(q[i] & 0x0F0F0F0Fu, dd, -8.f * dd, o + 2 * i);
-      cvt4((q[i] >> 4) & 0x0F0F0F0Fu, dd, -8.f * dd, o + 8 + 2 * i);
-    }
+    return GS{dd, -8.f * dd, 0.f, 0.f, 0};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    cvt4(q[i] & 0x0F0F0F0Fu, st.dl0, st.b0, o + 2 * i);
+    cvt4((q[i] >> 4) & 0x0F0F0F0Fu, st.dl0, st.b0, o + 8 + 2 * i);
   }
 };
 
@@ -133,12 +155,13 @@ template <> struct B2<GQK_IQ4_NL> {
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * kq + h)); gld<2>(&d, c + 64 * 128 + r * 16 + 2 * (2 * kq + h));
   }
-  __device__ void out(int, int, uint32_t (&o)[16], const GTabs& tb, int i) const {
+  __device__ GS prep(int, int) const {
     const float dd = g_h2f(d);
-    {
-      cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), dd, -128.f * dd, o + 2 * i);
-      cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), dd, -128.f * dd, o + 8 + 2 * i);
-    }
+    return GS{dd, -128.f * dd, 0.f, 0.f, 0};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), st.dl0, st.b0, o + 2 * i);
+    cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), st.dl0, st.b0, o + 8 + 2 * i);
   }
 };
 
@@ -151,14 +174,15 @@ template <> struct B2<GQK_Q5_0> {
     gld<16>(q, col16(c, r, b)); gld<4>(&qh, col16(c + 64 * 128, r, b >> 2) + 4 * (b & 3));
     gld<2>(&d, c + 64 * 160 + r * 16 + 2 * b);
   }
-  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int, int) const {
     const float dd = g_h2f(d);
-    {
-      const uint32_t hl = ((((qh >> (4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
-      const uint32_t hh = ((((qh >> (16 + 4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
-      cvt4((q[i] & 0x0F0F0F0Fu) | hl, dd, -16.f * dd, o + 2 * i);
-      cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | hh, dd, -16.f * dd, o + 8 + 2 * i);
-    }
+    return GS{dd, -16.f * dd, 0.f, 0.f, 0};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    const uint32_t hl = ((((qh >> (4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+    const uint32_t hh = ((((qh >> (16 + 4 * i)) & 0xFu) * 0x00204081u) & 0x01010101u) << 4;
+    cvt4((q[i] & 0x0F0F0F0Fu) | hl, st.dl0, st.b0, o + 2 * i);
+    cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | hh, st.dl0, st.b0, o + 8 + 2 * i);
   }
 };
 
@@ -170,10 +194,13 @@ template <> struct B2<GQK_Q8_0> {   // block b = 2 kq + h, 32 int8 in two 16-byt
     const int b = 2 * kq + h;
     gld<16>(q, col16(c, r, 2 * b)); gld<16>(q + 4, col16(c, r, 2 * b + 1)); gld<2>(&d, c + 64 * 256 + r * 16 + 2 * b);
   }
-  __device__ void out(int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int, int) const {
     const float dd = g_h2f(d);
-    cvt4(q[2 * i] ^ 0x80808080u, dd, -128.f * dd, o + 4 * i);
-    cvt4(q[2 * i + 1] ^ 0x80808080u, dd, -128.f * dd, o + 4 * i + 2);
+    return GS{dd, -128.f * dd, 0.f, 0.f, 0};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    cvt4(q[2 * i] ^ 0x80808080u, st.dl0, st.b0, o + 4 * i);
+    cvt4(q[2 * i + 1] ^ 0x80808080u, st.dl0, st.b0, o + 4 * i + 2);
   }
 };
 
@@ -184,16 +211,15 @@ template <> struct B2<GQK_Q2_K> {   // groups 2 kq, 2 kq + 1 share the 16 bytes 
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * (kq >> 1) + h)); gld<4>(&scw, c + 64 * 64 + r * 16 + 4 * kq); gld<4>(&dd, c + 64 * 80 + r * 4);
   }
-  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int, int h) const {
     const float d = g_h2f(dd), dmin = g_h2f(dd >> 16);
     const uint32_t s0 = (scw >> (8 * h)) & 0xFF, s1 = (scw >> (8 * (2 + h))) & 0xFF;
-    const float dl0 = d * (float)(s0 & 0xF), b0 = -(dmin * (float)(s0 >> 4));
-    const float dl1 = d * (float)(s1 & 0xF), b1 = -(dmin * (float)(s1 >> 4));
+    return GS{d * (float)(s0 & 0xF), -(dmin * (float)(s0 >> 4)), d * (float)(s1 & 0xF), -(dmin * (float)(s1 >> 4)), 0};
+  }
+  __device__ void out(const GS& st, int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
     const int j0 = 2 * (kq & 1);
-    {
-      cvt4((q[i] >> (2 * j0)) & 0x03030303u, dl0, b0, o + 2 * i);
-      cvt4((q[i] >> (2 * j0 + 2)) & 0x03030303u, dl1, b1, o + 8 + 2 * i);
-    }
+    cvt4((q[i] >> (2 * j0)) & 0x03030303u, st.dl0, st.b0, o + 2 * i);
+    cvt4((q[i] >> (2 * j0 + 2)) & 0x03030303u, st.dl1, st.b1, o + 8 + 2 * i);
   }
 };
 
@@ -208,16 +234,17 @@ template <> struct B2<GQK_Q3_K> {
     sb[0] = p[r]; sb[1] = p[64 + r]; sb[2] = p[128 + r];
     gld<2>(&d, c + 64 * 108 + r * 2);
   }
-  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int kq, int h) const {
     const float dd = g_h2f(d);
     const float dl0 = dd * (float)q3_scale(sb, 4 * kq + h), dl1 = dd * (float)q3_scale(sb, 4 * kq + 2 + h);
+    return GS{dl0, -4.f * dl0, dl1, -4.f * dl1, 0};
+  }
+  __device__ void out(const GS& st, int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
     const int j0 = 2 * (kq & 1), g0 = 2 * kq;
-    {
-      const uint32_t u0 = ((q[i] >> (2 * j0)) & 0x03030303u) | (((hm[i] >> g0) & 0x01010101u) << 2);
-      const uint32_t u1 = ((q[i] >> (2 * j0 + 2)) & 0x03030303u) | (((hm[i] >> (g0 + 1)) & 0x01010101u) << 2);
-      cvt4(u0, dl0, -4.f * dl0, o + 2 * i);
-      cvt4(u1, dl1, -4.f * dl1, o + 8 + 2 * i);
-    }
+    const uint32_t u0 = ((q[i] >> (2 * j0)) & 0x03030303u) | (((hm[i] >> g0) & 0x01010101u) << 2);
+    const uint32_t u1 = ((q[i] >> (2 * j0 + 2)) & 0x03030303u) | (((hm[i] >> (g0 + 1)) & 0x01010101u) << 2);
+    cvt4(u0, st.dl0, st.b0, o + 2 * i);
+    cvt4(u1, st.dl1, st.b1, o + 8 + 2 * i);
   }
 };
 
@@ -228,16 +255,10 @@ template <> struct B2<GQK_Q4_K> {   // low nibbles: sub-block 2 kq, high: 2 kq +
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * kq + h)); gld<16>(hdr, c + 64 * 128 + r * 16);
   }
-  __device__ void out(int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
-    int sc0, m0, sc1, m1;
-    k4_scale(hdr, 2 * kq, sc0, m0);
-    k4_scale(hdr, 2 * kq + 1, sc1, m1);
-    const float d = g_h2f(hdr[0]), dm = g_h2f(hdr[0] >> 16);
-    const float dl0 = d * (float)sc0, b0 = -(dm * (float)m0), dl1 = d * (float)sc1, b1 = -(dm * (float)m1);
-    {
-      cvt4(q[i] & 0x0F0F0F0Fu, dl0, b0, o + 2 * i);
-      cvt4((q[i] >> 4) & 0x0F0F0F0Fu, dl1, b1, o + 8 + 2 * i);
-    }
+  __device__ GS prep(int kq, int) const { return k4_prep(hdr, kq); }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    cvt4(q[i] & 0x0F0F0F0Fu, st.dl0, st.b0, o + 2 * i);
+    cvt4((q[i] >> 4) & 0x0F0F0F0Fu, st.dl1, st.b1, o + 8 + 2 * i);
   }
 };
 
@@ -248,16 +269,10 @@ template <> struct B2<GQK_Q5_K> {
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * kq + h)); gld<16>(qh, col16(c + 64 * 128, r, h)); gld<16>(hdr, c + 64 * 160 + r * 16);
   }
-  __device__ void out(int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
-    int sc0, m0, sc1, m1;
-    k4_scale(hdr, 2 * kq, sc0, m0);
-    k4_scale(hdr, 2 * kq + 1, sc1, m1);
-    const float d = g_h2f(hdr[0]), dm = g_h2f(hdr[0] >> 16);
-    const float dl0 = d * (float)sc0, b0 = -(dm * (float)m0), dl1 = d * (float)sc1, b1 = -(dm * (float)m1);
-    {
-      cvt4((q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq)) & 0x01010101u) << 4), dl0, b0, o + 2 * i);
-      cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq + 1)) & 0x01010101u) << 4), dl1, b1, o + 8 + 2 * i);
-    }
+  __device__ GS prep(int kq, int) const { return k4_prep(hdr, kq); }
+  __device__ void out(const GS& st, int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
+    cvt4((q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq)) & 0x01010101u) << 4), st.dl0, st.b0, o + 2 * i);
+    cvt4(((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * kq + 1)) & 0x01010101u) << 4), st.dl1, st.b1, o + 8 + 2 * i);
   }
 };
 
@@ -271,16 +286,17 @@ template <> struct B2<GQK_Q6_K> {   // groups 2 kq (ql bytes 64n + l) and 2 kq +
     gld<16>(qh, col16(c + 64 * 128, r, 2 * n + h));
     gld<4>(&scw, c + 64 * 192 + r * 16 + 4 * kq); gld<2>(&d, c + 64 * 208 + r * 2);
   }
-  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs&, int i) const {
+  __device__ GS prep(int, int h) const {
     const float dd = g_h2f(d);
     const float dl0 = dd * (float)(int8_t)((scw >> (8 * h)) & 0xFF), dl1 = dd * (float)(int8_t)((scw >> (8 * (2 + h))) & 0xFF);
+    return GS{dl0, -32.f * dl0, dl1, -32.f * dl1, 0};
+  }
+  __device__ void out(const GS& st, int kq, int, uint32_t (&o)[16], const GTabs&, int i) const {
     const int s = 4 * (kq & 1), t0 = 2 * (kq & 1);
-    {
-      const uint32_t u0 = ((a[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0)) & 0x03030303u) << 4);
-      const uint32_t u1 = ((b[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0 + 2)) & 0x03030303u) << 4);
-      cvt4(u0, dl0, -32.f * dl0, o + 2 * i);
-      cvt4(u1, dl1, -32.f * dl1, o + 8 + 2 * i);
-    }
+    const uint32_t u0 = ((a[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0)) & 0x03030303u) << 4);
+    const uint32_t u1 = ((b[i] >> s) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * t0 + 2)) & 0x03030303u) << 4);
+    cvt4(u0, st.dl0, st.b0, o + 2 * i);
+    cvt4(u1, st.dl1, st.b1, o + 8 + 2 * i);
   }
 };
 
@@ -291,14 +307,15 @@ template <> struct B2<GQK_IQ4_XS> {
   __device__ void load(const uint8_t* c, int r, int kq, int h) {
     gld<16>(q, col16(c, r, 2 * kq + h)); gld<8>(hdr, c + 64 * 128 + r * 8);
   }
-  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs& tb, int i) const {
+  __device__ GS prep(int kq, int h) const {
     const int g = 2 * kq + h;
     const int ls = (int)(((hdr[1] >> (4 * g)) & 0xF) | (((hdr[0] >> (16 + 2 * g)) & 3) << 4));
     const float dl = g_h2f(hdr[0]) * (float)(ls - 32);
-    {
-      cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), dl, -128.f * dl, o + 2 * i);
-      cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), dl, -128.f * dl, o + 8 + 2 * i);
-    }
+    return GS{dl, -128.f * dl, 0.f, 0.f, 0};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    cvt4(kv4(q[i] & 0x0F0F0F0Fu, tb), st.dl0, st.b0, o + 2 * i);
+    cvt4(kv4((q[i] >> 4) & 0x0F0F0F0Fu, tb), st.dl0, st.b0, o + 8 + 2 * i);
   }
 };
 
@@ -314,10 +331,15 @@ template <> struct B2<GQK_IQ3_S> {   // group g = 2 kq + h: 32 weights, magnitud
     gld<4>(&scb, c + 64 * 104 + r * 4);
     gld<2>(&d, c + 64 * 108 + r * 2);
   }
-  __device__ void out(int kq, int h, uint32_t (&o)[16], const GTabs& tb, int i) const {
+  __device__ GS prep(int kq, int h) const {
     const int g = 2 * kq + h;
     const float dl = g_h2f(d) * (float)(1 + 2 * (int)((scb >> (4 * g)) & 0xF));
     const uint32_t qhb = (uint32_t)(((uint64_t)qh[0] | ((uint64_t)qh[1] << 32)) >> (8 * g)) & 0xFF;
+    return GS{dl, 0.f, 0.f, 0.f, qhb};
+  }
+  __device__ void out(const GS& st, int, int, uint32_t (&o)[16], const GTabs& tb, int i) const {
+    const float dl = st.dl0;
+    const uint32_t qhb = st.aux;
     {
       const int l = i;
       const uint32_t qsw = qs[l >> 1] >> (16 * (l & 1));
@@ -349,9 +371,12 @@ struct GOut {
 // Tile geometry: BM tokens x BN weight rows per tile, a WGM x WGN grid of waves each owning
 // (BM / WGM) x (BN / WGN) outputs in 32 x 32 MFMA blocks.  Thread t decodes part t & 1 of weight
 // row t >> 1 each step, and stages AV 16-byte chunks of x.
-template <int BM_, int BN_, int WGM_, int WGN_>
+template <int BM_, int BN_, int WGM_, int WGN_, int XD_, int WD_>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NW = WGM * WGN, NT = 64 * NW;
+  // pipeline depth: x loaded XD steps, weights WD steps before the step that multiplies them
+  static constexpr int XD = XD_, WD = WD_, U = XD * WD / std::gcd(XD, WD);   // steps per unrolled trip
+  static_assert(XD >= 1 && XD <= 3 && WD >= 2 && WD <= 3 && (U == 2 || U == 3 || U == 6), "pipeline depths");
   static constexpr int MB = BM / WGM / 32, NB = BN / WGN / 32;   // 32 x 32 blocks per wave
   static constexpr int AV = BM * 8 / NT;                          // x chunks per thread per step
   static constexpr int CH = MB * NB * 4;                          // 16-byte accumulator chunks per thread
@@ -360,9 +385,16 @@ struct Geo {
   static_assert(BN * 2 == NT, "one thread per (weight row, part)");
   static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
 };
-typedef Geo<256, 256, 4, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
-typedef Geo<128, 128, 2, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
-typedef Geo<64, 128, 2, 2> GeoSmall;   // 33..64 tokens
+typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
+typedef Geo<128, 128, 2, 2, 1, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
+typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 17..64 tokens
+
+template <int S, class V>
+__device__ __forceinline__ V& pick(V& a, V& b, V& c) {
+  if constexpr (S == 0) return a;
+  else if constexpr (S == 1) return b;
+  else return c;
+}
 
 template <class GE, int T>
 __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
@@ -401,20 +433,30 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
   // (clamped to the last step).  Rows past M (x) and past the shard's rows (weights) hold clamped
   // copies of real data: they only reach accumulator entries that are never stored.
   const int last = k1 - 1;
-  uint4 av[AV];
-  B2<T> p0, p1;
-  auto xload = [&](int s) {
-    const uint4* ap = (const uint4*)(abase + (int64_t)s * GB_K);
+  constexpr int XD = GE::XD, WD = GE::WD;
+  // x of steps s + 1 .. s + XD and weights of steps s + 1 .. s + WD in flight (set j holds the
+  // steps j mod XD, j mod WD); separate variables picked at compile time, so they stay in registers
+  struct XS { v4u v[AV]; };   // clang vectors (not uint4's union), so the sets stay in registers
+  XS x0, x1, x2;
+  B2<T> w0, w1, w2;
+  // register sets are picked by compile-time index (S: std::integral_constant)
+  auto xload = [&](auto S, int s) __attribute__((always_inline)) {
+    const v4u* ap = (const v4u*)(abase + (int64_t)s * GB_K);
 #pragma unroll
-    for (int i = 0; i < AV; ++i) av[i] = ap[i];
+    for (int i = 0; i < AV; ++i) pick<decltype(S)::value>(x0, x1, x2).v[i] = ap[i];
   };
-  auto xstore = [&](int buf) {
-    uint4* as = (uint4*)(As + (buf * GE::BM + ar) * GB_LD + 8 * ac);
+  auto xstore = [&](auto S, int buf) __attribute__((always_inline)) {
+    v4u* as = (v4u*)(As + (buf * GE::BM + ar) * GB_LD + 8 * ac);
 #pragma unroll
-    for (int i = 0; i < AV; ++i) as[i] = av[i];
+    for (int i = 0; i < AV; ++i) as[i] = pick<decltype(S)::value>(x0, x1, x2).v[i];
   };
-  auto wload = [&](B2<T>& p, int s) { p.load(bbase + (int64_t)(s >> 2) * (64 * REC), brow, s & 3, h); };
-  auto wdecode = [&](const B2<T>& p, int s, uint32_t (&o)[16], int i) { p.out(s & 3, h, o, tb, i); };
+  auto wload = [&](auto S, int s) __attribute__((always_inline)) {
+    pick<decltype(S)::value>(w0, w1, w2).load(bbase + (int64_t)(s >> 2) * (64 * REC), brow, s & 3, h);
+  };
+  auto wprep = [&](auto S, int s) __attribute__((always_inline)) { return pick<decltype(S)::value>(w0, w1, w2).prep(s & 3, h); };
+  auto wdecode = [&](auto S, const GS& st, int s, uint32_t (&o)[16], int i) {
+    pick<decltype(S)::value>(w0, w1, w2).out(st, s & 3, h, o, tb, i);
+  };
   auto wstore = [&](const uint32_t (&o)[16], int buf) {
     uint16_t* bs = Bs + (buf * GE::BN + br) * GB_LD;
     uint4* d0 = (uint4*)(bs + B2<T>::off0(h));
@@ -424,48 +466,74 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
     d1[0] = make_uint4(o[8], o[9], o[10], o[11]);
     d1[1] = make_uint4(o[12], o[13], o[14], o[15]);
   };
-  auto step = [&](int s, const B2<T>& pd, B2<T>& pl) {
+  // step s = k0 + j (mod U): the sets that held step s (x stored, weights decoded during step
+  // s - 1) take the loads of steps s + XD and s + WD.
+  auto step = [&](auto J, int s) __attribute__((always_inline)) {
+    constexpr int j = decltype(J)::value;
     const int buf = (s - k0) & 1;
-    xload(min(s + 1, last));
-    wload(pl, min(s + 2, last));
+    xload(std::integral_constant<int, j % XD>{}, min(s + XD, last));
+    wload(std::integral_constant<int, j % WD>{}, min(s + WD, last));
     const uint16_t* as = As + (buf * GE::BM + wm * WTM + (lane & 31)) * GB_LD + 8 * (lane >> 5);
     const uint16_t* bs = Bs + (buf * GE::BN + wn * WTN + (lane & 31)) * GB_LD + 8 * (lane >> 5);
     uint32_t o[16];
+    GS st;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       v8bf af[MB], bf[NB];
 #pragma unroll
       for (int i = 0; i < MB; ++i) af[i] = *(const v8bf*)(as + 32 * i * GB_LD + 16 * kk);
 #pragma unroll
-      for (int j = 0; j < NB; ++j) bf[j] = *(const v8bf*)(bs + 32 * j * GB_LD + 16 * kk);
+      for (int j2 = 0; j2 < NB; ++j2) bf[j2] = *(const v8bf*)(bs + 32 * j2 * GB_LD + 16 * kk);
 #pragma unroll
       for (int i = 0; i < MB; ++i)
 #pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      wdecode(pd, s + 1, o, kk);
+        for (int j2 = 0; j2 < NB; ++j2)
+          acc[i][j2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j2], acc[i][j2], 0, 0, 0);
+      if (kk == 0) st = wprep(std::integral_constant<int, (j + 1) % WD>{}, s + 1);   // after the first MFMAs
+      wdecode(std::integral_constant<int, (j + 1) % WD>{}, st, s + 1, o, kk);
     }
-    xstore(buf ^ 1);
+    xstore(std::integral_constant<int, (j + 1) % XD>{}, buf ^ 1);
     wstore(o, buf ^ 1);
     __syncthreads();
   };
 
-  xload(k0);
-  wload(p0, k0);
-  wload(p1, min(k0 + 1, last));
+  xload(std::integral_constant<int, 0>{}, k0);
+  if constexpr (XD > 1) xload(std::integral_constant<int, 1>{}, min(k0 + 1, last));
+  if constexpr (XD > 2) xload(std::integral_constant<int, 2>{}, min(k0 + 2, last));
+  wload(std::integral_constant<int, 0>{}, k0);
+  wload(std::integral_constant<int, 1>{}, min(k0 + 1, last));
+  if constexpr (WD > 2) wload(std::integral_constant<int, 2>{}, min(k0 + 2, last));
   {
     uint32_t o[16];
-    xstore(0);
+    xstore(std::integral_constant<int, 0>{}, 0);
+    const GS st = wprep(std::integral_constant<int, 0>{}, k0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wdecode(p0, k0, o, i);
+    for (int i = 0; i < 4; ++i) wdecode(std::integral_constant<int, 0>{}, st, k0, o, i);
     wstore(o, 0);
   }
   __syncthreads();
+  // U = lcm(XD, WD) steps per trip, so every set index is a constant; then the last k1 - s < U
   int s = k0;
-  for (; s + 1 < k1; s += 2) {
-    step(s, p1, p0);
-    step(s + 1, p0, p1);
+  for (; s + GE::U <= k1; s += GE::U) {
+    step(std::integral_constant<int, 0>{}, s);
+    step(std::integral_constant<int, 1>{}, s + 1);
+    if constexpr (GE::U > 2) step(std::integral_constant<int, 2>{}, s + 2);
+    if constexpr (GE::U > 3) {
+      step(std::integral_constant<int, 3>{}, s + 3);
+      step(std::integral_constant<int, 4>{}, s + 4);
+      step(std::integral_constant<int, 5>{}, s + 5);
+    }
   }
-  if (s < k1) step(s, p1, p0);
+  if (s < k1) {
+    step(std::integral_constant<int, 0>{}, s);
+    if constexpr (GE::U > 2)
+      if (s + 1 < k1) step(std::integral_constant<int, 1>{}, s + 1);
+    if constexpr (GE::U > 3) {
+      if (s + 2 < k1) step(std::integral_constant<int, 2>{}, s + 2);
+      if (s + 3 < k1) step(std::integral_constant<int, 3>{}, s + 3);
+      if (s + 4 < k1) step(std::integral_constant<int, 4>{}, s + 4);
+    }
+  }
 
   // C block (i, j): lane -> weight row 32 j + (lane & 31), tokens 8 (v / 4) + 4 (lane / 32) + v % 4
   const int nvalid = dsc[D_NVALID];
@@ -486,38 +554,68 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
       for (int j = 0; j < NB; ++j) store_y(i, j, acc[i][j]);
     return;
   }
-  // Partial slot layout: chunk c (elements 4 (c & 3) .. of acc[c / (4 NB)][(c / 4) % NB]) of thread
-  // tid at ((slot * CH + c) * NT + tid) * 16, so every store and load is coalesced.
+  // Partial slot layout: chunk (i, j, e) = elements 4 e .. 4 e + 3 of acc[i][j] (four consecutive
+  // tokens of one weight row) of thread tid at ((slot * CH + (i NB + j) 4 + e) * NT + tid) * 16, so
+  // every store and load is coalesced.  Chunks of tokens >= M or rows >= nvalid are not written.
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       go.part + (int64_t)go.slot0 * GE::SLOT, 0, go.nc * GE::SLOT * 4, GQK_GB_WORD3);
+  auto live = [&](int i, int j, int e) {
+    return m0 + wm * WTM + 32 * i + 8 * e + 4 * (lane >> 5) < M && wn * WTN + 32 * j + (lane & 31) < nvalid;
+  };   // chunks that reach y
+  auto own = [&](int i, int j, int e) {
+    const v16f& a = acc[i][j];
+    return v4f{a[4 * e], a[4 * e + 1], a[4 * e + 2], a[4 * e + 3]};
+  };
+  auto slot_off = [&](int q, int i, int j, int e) { return ((q * GE::CH + (i * NB + j) * 4 + e) * NT + tid) * 16; };
+  // Contributors count themselves on the tile's counter once their partial is complete; the last
+  // one sums.  A contributor that finds the other nc - 1 already counted is the last for sure: it
+  // skips writing its own partial and sums at once.
+  if (tid == 0) *flag = __hip_atomic_load(go.ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const bool last_now = *flag == go.nc - 1;
+  __syncthreads();
+  if (!last_now) {
 #pragma unroll
-  for (int c = 0; c < GE::CH; ++c) {
-    const v16f& a = acc[c / (4 * NB)][(c / 4) % NB];
-    const v4f q = {a[4 * (c & 3)], a[4 * (c & 3) + 1], a[4 * (c & 3) + 2], a[4 * (c & 3) + 3]};
-    __builtin_amdgcn_raw_buffer_store_b128(q, rs, ((go.self * GE::CH + c) * NT + tid) * 16, 0, GQK_GB_SC1);
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (live(i, j, e)) __builtin_amdgcn_raw_buffer_store_b128(own(i, j, e), rs, slot_off(go.self, i, j, e), 0, GQK_GB_SC1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this workgroup's partial is complete
+    __syncthreads();
+    if (tid == 0) *flag = __hip_atomic_fetch_add(go.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*flag != go.nc - 1) return;
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this workgroup's partial is complete
-  __syncthreads();
-  if (tid == 0) *flag = __hip_atomic_fetch_add(go.ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (*flag != go.nc - 1) return;
   asm volatile("" ::: "memory");
-  // the last contributor: slot 0 + slot 1 + ... in k order, one 32 x 32 block at a time
+  // the last contributor: slot 0 + slot 1 + ... in k order (its own from registers), one 32 x 32
+  // block at a time, the loads of QB slots in flight together.  Loads are unconditional (slot
+  // clamped to the last): chunks never written only reach sums that are never stored.
+  constexpr int QB = GE::CH >= 32 ? 2 : 4;
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int c0 = (i * NB + j) * 4;
       v4f sum[4];
+      for (int q0 = 0; q0 < go.nc; q0 += QB) {
+        v4f t[QB][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sum[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((c0 + e) * NT + tid) * 16, 0, GQK_GB_SC1);
-      for (int q = 1; q < go.nc; ++q) {
-        v4f t[4];
+        for (int b = 0; b < QB; ++b)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          t[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((q * GE::CH + c0 + e) * NT + tid) * 16, 0, GQK_GB_SC1);
+          for (int e = 0; e < 4; ++e)
+            t[b][e] = __builtin_amdgcn_raw_buffer_load_b128(rs, slot_off(min(q0 + b, go.nc - 1), i, j, e), 0, GQK_GB_SC1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] += t[e];
+        for (int b = 0; b < QB; ++b) {
+          const int q = q0 + b;
+          if (q < go.nc) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const v4f v = q == go.self ? own(i, j, e) : t[b][e];
+              sum[e] = q == 0 ? v : sum[e] + v;
+            }
+          }
+        }
       }
       const v16f a = {sum[0][0], sum[0][1], sum[0][2], sum[0][3], sum[1][0], sum[1][1], sum[1][2], sum[1][3],
                       sum[2][0], sum[2][1], sum[2][2], sum[2][3], sum[3][0], sum[3][1], sum[3][2], sum[3][3]};
@@ -545,14 +643,14 @@ __device__ __forceinline__ void gb_map(int i, int n_desc, int nmb, int& d, int& 
 
 // Persistent schedule over G workgroups (all resident: two waves per SIMD, so at most 256 registers
 // a lane; no workgroup ever waits for another, so residency is a matter of speed only): the first floor(T / G) * G tiles whole,
-// dealt round robin; the remaining R tiles' k-steps split evenly over G_sk = min(G, R * steps)
-// workgroups (stream-K), tiles shared by several workgroups combined through partial slots.
+// dealt round robin; the remaining R tiles' k-steps split evenly over gsk workgroups (stream-K,
+// gb_stream_k_workgroups), tiles shared by several workgroups combined through partial slots.
 template <class GE, int ONLY>
 __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_sk_kernel(const uint8_t* __restrict__ packed,
                                                           const int32_t* __restrict__ desc, int n_desc,
                                                           const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                           uint16_t* __restrict__ y, int64_t ldy, float* part, int* ctr,
-                                                          int G) {
+                                                          int G, int gsk) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[GE::LDS + GB_TAB_BYTES + 16];
   uint16_t* As = (uint16_t*)lds;
   uint16_t* Bs = As + 2 * GE::BM * GB_LD;
@@ -594,7 +692,6 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
   const int tfull = (T / G) * G;
   const int R = T - tfull;
   const int64_t I = (int64_t)R * nsteps;
-  const int gsk = (int)min<int64_t>(G, I);
   const int w = blockIdx.x;
   auto owner = [&](int64_t i) { return (int)(((i + 1) * gsk + I - 1) / I - 1); };   // workgroup of step i
   int64_t it = 0, end = 0;
@@ -645,13 +742,19 @@ static int gb_cus() {
 static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : 2); }
 static int gb_slot_floats(int bm) { return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : GeoSmall::SLOT; }
 
+// Stream-K workgroups for R remainder tiles of 4 nb steps: all G, or one per step when there are
+// fewer steps.  (Longer ranges, i.e. fewer contributors per tile, measured slower.)
+static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb) {
+  return std::max<int64_t>(1, std::min<int64_t>(G, R * 4 * nb));
+}
+
 int64_t gemm_workspace(int bm, int n_desc, int M, int nb) {
   const int G = gb_workgroups(bm);
   if (G <= 0) return -1;
   const int64_t T = (int64_t)n_desc * ((M + bm - 1) / bm);
   const int64_t R = T % G;
   if (R == 0) return 0;
-  const int64_t gsk = std::min<int64_t>(G, R * 4 * nb);
+  const int64_t gsk = gb_stream_k_workgroups(G, R, nb);
   return ((int64_t)G * 4 + 255) / 256 * 256 + (R + gsk - 1) * gb_slot_floats(bm) * 4;
 }
 
@@ -664,17 +767,17 @@ static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const 
   if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255))) return GQK_ERR_SHAPE;
   int* ctr = (int*)ws;
   float* part = need > 0 ? (float*)((char*)ws + ((int64_t)G * 4 + 255) / 256 * 256) : nullptr;
-  // G workgroups when there are at least G tiles; else every stream-K participant,
-  // min(G, T * steps) (the kernel splits the steps of all T tiles over that many)
+  // G workgroups when there are at least G tiles; else the stream-K participants only
   const int64_t T = (int64_t)n_desc * ((M + GE::BM - 1) / GE::BM);
-  dim3 grid((unsigned)(T >= G ? G : std::min<int64_t>(G, T * 4 * nb)));
+  const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb);
+  dim3 grid((unsigned)(T >= G ? G : gsk));
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G); return GQK_OK;
+#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G, gsk); return GQK_OK;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemm_sk_kernel<GE, 0>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G);
+      hipLaunchKernelGGL((gemm_sk_kernel<GE, 0>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G, gsk);
   }
   return GQK_OK;
 }
