@@ -44,6 +44,8 @@ int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return 
 
 }  // namespace
 
+void gqk_set_last_error(const char* msg) { g_err = msg ? msg : ""; }
+
 extern "C" {
 
 const char* gqk_last_error(void) { return g_err.c_str(); }

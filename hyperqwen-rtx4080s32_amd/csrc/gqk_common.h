@@ -131,6 +131,11 @@ enum {
   D_CTR = 11,     // GEMV split-K: arrival counter of the row's tile (index into the counters)
 };
 
+#ifdef __cplusplus
+// sets the calling thread's gqk_last_error() message (library-internal; defined in gqk_api.hip)
+void gqk_set_last_error(const char* msg);
+#endif
+
 // forms of a grouped launch
 #define GQK_FORM_GEMV 1   // M <= 16: in-register decode, MFMA 4x4x4 per sub-block, fp32 epilogue
 #define GQK_FORM_GEMM 2   // M > 16: tile decoded to bf16 in LDS, MFMA 32x32x16

@@ -22,7 +22,9 @@ GQK_DTYPE_F32, GQK_DTYPE_BF16, GQK_DTYPE_F16 = 0, 1, 2
 
 # every entry point include/gguf_hip.h declares
 EXPORTS = ("gqk_last_error", "gqk_version", "gqk_type_info", "gqk_dequantize", "gqk_tiles_bytes", "gqk_repack",
-           "gqk_unrepack", "gqk_plan", "gqk_linear_workspace_bytes", "gqk_linear")
+           "gqk_unrepack", "gqk_plan", "gqk_linear_workspace_bytes", "gqk_linear", "gqk_ggml_type_size",
+           "gqk_gguf_open", "gqk_gguf_close", "gqk_gguf_info", "gqk_gguf_tensor_at", "gqk_gguf_find_tensor",
+           "gqk_gguf_kv_at", "gqk_gguf_find_kv", "gqk_gguf_kv_string", "gqk_gguf_upload_tiles")
 
 
 class GqkShard(ctypes.Structure):
@@ -42,6 +44,18 @@ class GqkPlanInfo(ctypes.Structure):
     @classmethod
     def from_tuple(cls, t) -> "GqkPlanInfo":
         return cls(*t)
+
+
+class GqkGgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("ggml_type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("dims", ctypes.c_int64 * 4), ("offset", ctypes.c_int64), ("nbytes", ctypes.c_int64),
+                ("data", ctypes.c_void_p)]
+
+
+class GqkGgufKv(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("type", ctypes.c_int32), ("array_type", ctypes.c_int32),
+                ("count", ctypes.c_int64), ("i64", ctypes.c_int64), ("f64", ctypes.c_double),
+                ("data", ctypes.c_void_p)]
 
 
 class GqkError(RuntimeError):
@@ -71,6 +85,18 @@ def _load() -> ctypes.CDLL:
                            ctypes.POINTER(GqkPlanInfo)]),
         "gqk_linear_workspace_bytes": (i64, [ctypes.POINTER(GqkPlanInfo), i32]),
         "gqk_linear": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, i64, vp]),
+        "gqk_ggml_type_size": (i32, [i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
+        "gqk_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "gqk_gguf_close": (None, [vp]),
+        "gqk_gguf_info": (i32, [vp, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+                                ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+                                ctypes.POINTER(ctypes.c_int32)]),
+        "gqk_gguf_tensor_at": (i32, [vp, i64, ctypes.POINTER(GqkGgufTensor)]),
+        "gqk_gguf_find_tensor": (i64, [vp, ctypes.c_char_p]),
+        "gqk_gguf_kv_at": (i32, [vp, i64, ctypes.POINTER(GqkGgufKv)]),
+        "gqk_gguf_find_kv": (i64, [vp, ctypes.c_char_p]),
+        "gqk_gguf_kv_string": (i32, [vp, i64, i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)]),
+        "gqk_gguf_upload_tiles": (i32, [vp, i64, vp, i64, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

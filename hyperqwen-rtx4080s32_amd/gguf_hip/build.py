@@ -16,7 +16,7 @@ REPO = os.path.dirname(ROOT)
 CSRC = os.path.join(ROOT, "csrc")
 BUILD = os.path.join(ROOT, "_build")
 LIB = os.path.join(PKG, "libgqk.so")
-SOURCES = ("gqk_api.hip", "gqk_codec.hip", "gqk_gemv.hip", "gqk_gemm.hip")
+SOURCES = ("gqk_api.hip", "gqk_codec.hip", "gqk_gemv.hip", "gqk_gemm.hip", "gqk_gguf.cpp")
 ARCH = os.environ.get("GQK_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -36,12 +36,12 @@ def _run(cmd: list[str]) -> None:
 
 
 def build(jobs: int | None = None) -> str:
-    """Compile every HIP source and link libgqk.so (always rebuilds); returns the library path."""
+    """Compile every source (HIP kernels; the host-only GGUF reader) and link libgqk.so (always rebuilds); returns the library path."""
     os.makedirs(BUILD, exist_ok=True)
     objs = []
     cmds = []
     for src in SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=jobs or min(len(cmds), os.cpu_count() or 4)) as ex:

@@ -186,11 +186,21 @@ def prepare_grouped_layer(tiles_list: list[torch.Tensor], n_outs: list[int], wty
         if t.numel() != tiles_bytes(wt, n, K):
             raise ValueError(f"prepare_grouped_layer: tiles of a {n} x {K} shard of type {wt} have {t.numel()} bytes")
     packed = torch.cat([t.reshape(-1) for t in tiles_list]) if len(tiles_list) > 1 else tiles_list[0].reshape(-1)
+    return grouped_layer_from_packed(packed, n_outs, wtypes, K, target_wgs)
+
+
+def grouped_layer_from_packed(packed: torch.Tensor, n_outs: list[int], wtypes: list[int], K: int,
+                              target_wgs: int = 0) -> GroupedLayer:
+    """A grouped layer over a buffer that already holds the shards' tiles back to back (the
+    GGUF load path uploads each tensor straight into its slice)."""
+    sizes = [tiles_bytes(wt, n, K) for n, wt in zip(n_outs, wtypes)]
+    if packed.dtype != torch.uint8 or packed.dim() != 1 or packed.numel() != sum(sizes):
+        raise ValueError(f"grouped_layer_from_packed: packed must be uint8 [{sum(sizes)}]")
     views, shards, off = [], [], 0
-    for t, n, wt in zip(tiles_list, n_outs, wtypes):
-        views.append(packed[off:off + t.numel()])
+    for size, n, wt in zip(sizes, n_outs, wtypes):
+        views.append(packed[off:off + size])
         shards.append((wt, n, off))
-        off += t.numel()
+        off += size
     gl = GroupedLayer(packed, views, list(n_outs), list(wtypes), K)
     ws = 0
     for m in GEMV_BUCKETS + GEMM_PLAN_M:

@@ -100,9 +100,8 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
              int64_t desc_capacity, gqk_plan_info* info);
 
 /* Device workspace bytes gqk_linear needs for this plan at M batch rows (0: none; < 0: error).
- * GEMV plans with split-K need info->workspace_bytes; the 256-token GEMM form (info->bm == 256)
- * needs room for its stream-K partial tiles, which depends on M and on the current device's CU
- * count.  Replaces the reference's transient split-K partials (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
+ * GEMV plans with split-K need info->workspace_bytes; GEMM plans need room for their stream-K
+ * partial tiles, which depends on M and on the current device's CU count.  Replaces the reference's transient split-K partials (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
 int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
 
 /* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T over the grouped layer's shards (columns in shard
@@ -110,11 +109,78 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
  * least gqk_linear_workspace_bytes(info, M) bytes of 256-byte aligned device memory (NULL when
  * that is 0) holding arrival counters (first) and fp32 partials; it must be zero-filled before
  * its first use, every launch leaves the counters at zero again, and launches sharing one
- * workspace must not overlap in time.  M must be <= info->m_max (and > 32 for a GEMM plan).  Replaces the grouped op
+ * workspace must not overlap in time.  M must be <= info->m_max (and > 16 for a GEMM plan).  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
                int M, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- GGUF v3 files: the load path ----------------------------------------------------------
+ * The reference's tensors come from vLLM's GGUF loader (gguf-py 0.17.1 GGUFReader,
+ * gguf-plugin/requirements.txt:1) and are repacked at load time by _create_tiles
+ * (gguf-plugin/patches/gguf-tiles-all-types.patch:59-131).  Here a C++ reader maps the file read
+ * only; tensor data is never copied on the host. */
+typedef struct gqk_gguf gqk_gguf; /* an open GGUF file (immutable: safe to share across threads) */
+
+/* GGUF metadata value types */
+#define GQK_GGUF_UINT8 0
+#define GQK_GGUF_INT8 1
+#define GQK_GGUF_UINT16 2
+#define GQK_GGUF_INT16 3
+#define GQK_GGUF_UINT32 4
+#define GQK_GGUF_INT32 5
+#define GQK_GGUF_FLOAT32 6
+#define GQK_GGUF_BOOL 7
+#define GQK_GGUF_STRING 8
+#define GQK_GGUF_ARRAY 9
+#define GQK_GGUF_UINT64 10
+#define GQK_GGUF_INT64 11
+#define GQK_GGUF_FLOAT64 12
+
+typedef struct gqk_gguf_tensor {
+  const char* name;   /* NUL-terminated, owned by the handle */
+  int32_t ggml_type;
+  int32_t n_dims;
+  int64_t dims[4];    /* GGUF order: dims[0] = weights per row (K), dims[1] = rows (N); unused = 1 */
+  int64_t offset;     /* absolute byte offset of the data in the file */
+  int64_t nbytes;     /* packed bytes; -1 for a type without a fixed block size here */
+  const void* data;   /* host pointer into the read-only mapping (NULL when nbytes < 0) */
+} gqk_gguf_tensor;
+
+typedef struct gqk_gguf_kv {
+  const char* key;    /* NUL-terminated, owned by the handle */
+  int32_t type;       /* GQK_GGUF_* */
+  int32_t array_type; /* element type of an ARRAY */
+  int64_t count;      /* 1 for a scalar, bytes of a STRING, elements of an ARRAY */
+  int64_t i64;        /* integer and BOOL scalars (UINT64 as its bit pattern) */
+  double f64;         /* FLOAT32 / FLOAT64 scalars */
+  const void* data;   /* STRING bytes (not NUL-terminated) or the first ARRAY element (mapping) */
+} gqk_gguf_kv;
+
+/* (weights per block, bytes per block) of a GGML type: gguf.GGML_QUANT_SIZES
+ * (gguf-plugin/patches/gguf-prefill-dispatch.patch:42-45 reads it for the dequant shape). */
+int gqk_ggml_type_size(int ggml_type, int32_t* block, int32_t* bytes);
+
+/* Map and parse a GGUF v3 file (GGUFReader(path) in gguf-py).  *out is NULL on failure. */
+int gqk_gguf_open(const char* path, gqk_gguf** out);
+void gqk_gguf_close(gqk_gguf* f);
+/* Counts, alignment (general.alignment, default 32), data-section offset and version. */
+int gqk_gguf_info(const gqk_gguf* f, int64_t* n_tensors, int64_t* n_kv, int64_t* alignment, int64_t* data_offset,
+                  int32_t* version);
+/* Tensor info i (GGUFReader.tensors[i]); index of a tensor by name, -1 when absent. */
+int gqk_gguf_tensor_at(const gqk_gguf* f, int64_t i, gqk_gguf_tensor* out);
+int64_t gqk_gguf_find_tensor(const gqk_gguf* f, const char* name);
+/* Metadata key/value i (GGUFReader.fields); index of a key, -1 when absent; string j of a STRING
+ * (j = 0) or of an ARRAY of strings. */
+int gqk_gguf_kv_at(const gqk_gguf* f, int64_t i, gqk_gguf_kv* out);
+int64_t gqk_gguf_find_kv(const gqk_gguf* f, const char* key);
+int gqk_gguf_kv_string(const gqk_gguf* f, int64_t i, int64_t j, const char** s, int64_t* len);
+
+/* Load path of one quantized matrix: its raw rows from the mapping into `staging` (device, at
+ * least nbytes), then gqk_repack into `tiles` (gqk_tiles_bytes(type, dims[1], dims[0]) bytes), both
+ * on `stream`.  The copy reads pageable host memory, so it returns once the rows are staged. */
+int gqk_gguf_upload_tiles(const gqk_gguf* f, int64_t i, void* staging, int64_t staging_bytes, void* tiles,
+                          void* stream);
 
 #ifdef __cplusplus
 }

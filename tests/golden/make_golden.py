@@ -12,14 +12,19 @@ never travels).
   (post-patch lines of ``gguf-plugin/patches/gguf-iq3s-grid-top-magnitude.patch:18-138``, in
   quarter units).
 * ``iq4_kvalues.npy``: the IQ4 value table as written at ``gguf-plugin/gluon/iq4xs.py:36``.
+* ``qwen35_iq3s_tensors.json``: the tensor table (name, GGUF dims, GGML type) of the published
+  IQ3_S model file as the reference records it in ``gguf-plugin/iq3s-tensor-names.json`` (read from
+  that file's header; used by the reference's CPU gate, ``gguf-plugin/test_gguf_rco_cpu.py:84-127``).
 
-Usage: ``python tests/golden/make_golden.py``
+Usage: ``python tests/golden/make_golden.py`` (everything) or ``... tensors`` (the table only)
 """
 from __future__ import annotations
 
 import importlib.util
+import json
 import os
 import re
+import sys
 
 import numpy as np
 
@@ -54,7 +59,21 @@ def kvalues_from_text() -> np.ndarray:
     return np.array([int(v) for v in m.group(1).split(",")], dtype=np.int8)
 
 
+def tensor_table() -> None:
+    doc = json.load(open(os.path.join(REF, "iq3s-tensor-names.json"), encoding="utf-8"))
+    out = {"file": doc["file"], "architecture": doc["architecture"],
+           "tensors": [{"name": t["name"], "dims": t["dims"], "type": t["type"]} for t in doc["tensors"]]}
+    with open(os.path.join(HERE, "qwen35_iq3s_tensors.json"), "w", encoding="utf-8") as f:
+        f.write('{"file": %s, "architecture": %s, "tensors": [\n' % (json.dumps(out["file"]), json.dumps(out["architecture"])))
+        f.write(",\n".join(json.dumps(t) for t in out["tensors"]))
+        f.write("\n]}\n")
+
+
 def main() -> None:
+    if sys.argv[1:] == ["tensors"]:
+        tensor_table()
+        return
+    tensor_table()
     kq = _load_kq_ref()
     rng = np.random.default_rng(3)
     for wt in (8, 11, 13, 14):

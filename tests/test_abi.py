@@ -17,7 +17,7 @@ def test_exports_every_declared_symbol():
     from gguf_hip import _lib
 
     hdr = open(os.path.join(REPO, "include", "gguf_hip.h"), encoding="utf-8").read()
-    declared = set(re.findall(r"^\s*(?:const\s+char\*|int64_t|int)\s+(gqk_\w+)\s*\(", hdr, re.M))
+    declared = set(re.findall(r"^\s*(?:const\s+char\*|int64_t|int|void)\s+(gqk_\w+)\s*\(", hdr, re.M))
     assert declared == set(_lib.EXPORTS)
     for name in declared:
         assert hasattr(_lib.lib, name)
