@@ -235,7 +235,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
 }
 
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
-               int M, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream) {
+               int M, void* y, int64_t ldy, const void* bias, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!info) return fail(GQK_ERR_ARG, "linear: info is NULL");
   if (M < 0) return fail(GQK_ERR_SHAPE, "linear: M=%d", M);
   if (M == 0) return GQK_OK;
@@ -263,7 +263,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
       partials = (float*)((char*)workspace + cb);
     }
     int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw, y,
-                              ldy, partials, counters, info->split, info->n_total, (hipStream_t)stream);
+                              ldy, bias, partials, counters, info->split, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }
@@ -271,7 +271,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     if (M <= GQK_GEMV_MAX_M) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
     if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
     int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
-                              info->bm, workspace, workspace_bytes, (hipStream_t)stream);
+                              bias, info->bm, workspace, workspace_bytes, (hipStream_t)stream);
     if (rc == GQK_ERR_SHAPE)
       return fail(rc, "linear: GEMM workspace %lld bytes < %lld (or not 256-byte aligned)", (long long)workspace_bytes,
                   (long long)gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb));

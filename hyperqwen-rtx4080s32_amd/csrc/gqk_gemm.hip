@@ -400,7 +400,8 @@ template <class GE, int T>
 __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed, const int32_t* __restrict__ dsc,
                                              const uint16_t* __restrict__ x, int64_t ldx, int M, int m0, int k0,
                                              int k1, const GOut& go, uint16_t* __restrict__ y, int64_t ldy,
-                                             uint16_t* As, uint16_t* Bs, int* flag, const GTabs& tb) {
+                                             const uint16_t* __restrict__ bias, uint16_t* As, uint16_t* Bs, int* flag,
+                                             const GTabs& tb) {
   constexpr int REC = gqk_layout<T>::REC;
   constexpr int MB = GE::MB, NB = GE::NB, AV = GE::AV, NT = GE::NT;
   constexpr int WTM = GE::BM / GE::WGM, WTN = GE::BN / GE::WGN;
@@ -541,10 +542,12 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
   auto store_y = [&](int i, int j, const v16f& a) {
     const int r = wn * WTN + 32 * j + (lane & 31);
     if (r >= nvalid) return;
+    // the layer bias (bf16 per output column) joins before the one rounding to bf16
+    const float bv = bias != nullptr ? __builtin_bit_cast(float, (uint32_t)bias[col0 + r] << 16) : 0.f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int t = m0 + wm * WTM + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      if (t < M) y[(int64_t)t * ldy + col0 + r] = __builtin_bit_cast(uint16_t, (__bf16)a[v]);
+      if (t < M) y[(int64_t)t * ldy + col0 + r] = __builtin_bit_cast(uint16_t, (__bf16)(a[v] + bv));
     }
   };
   if (go.part == nullptr) {
@@ -649,7 +652,8 @@ template <class GE, int ONLY>
 __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_sk_kernel(const uint8_t* __restrict__ packed,
                                                           const int32_t* __restrict__ desc, int n_desc,
                                                           const uint16_t* __restrict__ x, int64_t ldx, int M,
-                                                          uint16_t* __restrict__ y, int64_t ldy, float* part, int* ctr,
+                                                          uint16_t* __restrict__ y, int64_t ldy,
+                                                          const uint16_t* __restrict__ bias, float* part, int* ctr,
                                                           int G, int gsk) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[GE::LDS + GB_TAB_BYTES + 16];
   uint16_t* As = (uint16_t*)lds;
@@ -684,7 +688,7 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) voi
     const int type = dsc[D_TYPE];
 #define RUN(TY)                                                                                          \
     if ((ONLY == 0 || ONLY == TY) && type == TY)                                                         \
-      gemm_tile_sk<GE, TY>(packed, dsc, x, ldx, M, mb * GE::BM, k0, k1, go, y, ldy, As, Bs, flag, tb);
+      gemm_tile_sk<GE, TY>(packed, dsc, x, ldx, M, mb * GE::BM, k0, k1, go, y, ldy, bias, As, Bs, flag, tb);
     RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
     RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
@@ -760,7 +764,8 @@ int64_t gemm_workspace(int bm, int n_desc, int M, int nb) {
 
 template <class GE>
 static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
-                     const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, void* ws, int64_t ws_bytes) {
+                     const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, const uint16_t* bias, void* ws,
+                     int64_t ws_bytes) {
   const int G = gb_workgroups(GE::BM);
   if (G <= 0) return GQK_ERR_HIP;
   const int64_t need = gemm_workspace(GE::BM, n_desc, M, nb);
@@ -772,25 +777,27 @@ static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const 
   const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb);
   dim3 grid((unsigned)(T >= G ? G : gsk));
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G, gsk); return GQK_OK;
+#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, bias, part, ctr, G, gsk); return GQK_OK;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemm_sk_kernel<GE, 0>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, part, ctr, G, gsk);
+      hipLaunchKernelGGL((gemm_sk_kernel<GE, 0>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, bias, part, ctr, G, gsk);
   }
   return GQK_OK;
 }
 
 int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int64_t K, void* y, int64_t ldy, int bm, void* ws, int64_t ws_bytes, hipStream_t st) {
+                int M, int64_t K, void* y, int64_t ldy, const void* bias, int bm, void* ws, int64_t ws_bytes,
+                hipStream_t st) {
   const int nb = (int)(K / 256);
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
+  const uint16_t* bb = (const uint16_t*)bias;
   switch (bm) {
-    case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
-    case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
-    case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, ws, ws_bytes);
+    case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
+    case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
+    case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
     default: return GQK_ERR_FORM;
   }
 }

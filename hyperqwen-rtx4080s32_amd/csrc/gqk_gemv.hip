@@ -527,8 +527,8 @@ constexpr int gemv_waves() {
 template <int G, int ONLY>
 __global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>())))
 void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
-                 int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, float* __restrict__ part,
-                 int* __restrict__ ctr, int64_t n_total, int split) {
+                 int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ bias,
+                 float* __restrict__ part, int* __restrict__ ctr, int split) {
   constexpr int MPAD = 4 * G;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
@@ -572,6 +572,8 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
 
   const bool row_ok = lane < dsc[D_NVALID];
   const int64_t col = (int64_t)dsc[D_COL0] + lane;
+  // the layer bias (bf16 per output column) joins before the one rounding to bf16
+  const float bv = bias != nullptr && row_ok ? __builtin_bit_cast(float, (uint32_t)bias[col] << 16) : 0.f;
   if (part == nullptr) {
     if (row_ok)
 #pragma unroll
@@ -579,7 +581,7 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int t = 4 * g + i;
-          if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)acc[g][i]);
+          if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)(acc[g][i] + bv));
         }
     return;
   }
@@ -625,41 +627,42 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 4 * g + i;
-        if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)a[g][i]);
+        if (t < M) y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)(a[g][i] + bv));
       }
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
 template <int G>
 static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
-                     const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, float* part, int* ctr,
-                     int64_t n_total, int split) {
+                     const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, const uint16_t* bias,
+                     float* part, int* ctr, int split) {
   const bool iq = only == 0 || only == GQK_IQ4_NL || only == GQK_IQ4_XS || only == GQK_IQ3_S;
   const size_t lds = (size_t)gemv_lds_bytes<G>(nw, iq);
   const dim3 block(64 * nw);
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split); return;
+#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr, split); return;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, part, ctr, n_total, split);
+      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr, split);
   }
 }
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, int nw, void* y, int64_t ldy, float* partials, int* counters, int split, int64_t n_total,
+                int M, int G, int nw, void* y, int64_t ldy, const void* bias, float* partials, int* counters, int split,
                 hipStream_t st) {
   if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
   dim3 grid(n_desc);
   float* part = split > 1 ? partials : nullptr;
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
+  const uint16_t* bb = (const uint16_t*)bias;
   switch (G) {
-    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
-    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, part, counters, n_total, split); break;
+    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
+    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
+    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
     default: return GQK_ERR_FORM;
   }
   return GQK_OK;

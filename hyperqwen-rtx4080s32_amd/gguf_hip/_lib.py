@@ -84,7 +84,7 @@ def _load() -> ctypes.CDLL:
         "gqk_plan": (i32, [ctypes.POINTER(GqkShard), i32, i64, i32, i32, ctypes.POINTER(ctypes.c_int32), i64,
                            ctypes.POINTER(GqkPlanInfo)]),
         "gqk_linear_workspace_bytes": (i64, [ctypes.POINTER(GqkPlanInfo), i32]),
-        "gqk_linear": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, i64, vp]),
+        "gqk_linear": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, vp, i64, vp]),
         "gqk_ggml_type_size": (i32, [i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
         "gqk_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "gqk_gguf_close": (None, [vp]),

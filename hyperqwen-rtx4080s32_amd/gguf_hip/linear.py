@@ -9,9 +9,10 @@ it (the plugin itself is not vendored):
   run of shards is packed into one buffer with its launch plans, and the raw rows are freed.
   All eleven types are tile types here, so a merged layer is always one run (one launch).
 * ``apply(layer, x, bias)`` (``gguf-plugin/patches/gguf-tiles-grouped.patch:131-171``,
-  ``gguf-plugin/patches/gguf-iq3s-tiles.patch:98-136``): same-type or grouped -> one op; an
-  unquantized shard beside quantized ones is multiplied as it is and concatenated; then
-  ``out.add_(bias)``.  M = 0 returns an empty [0, N] tensor.
+  ``gguf-plugin/patches/gguf-iq3s-tiles.patch:98-136``): same-type or grouped -> one op, with
+  a bf16 bias fused into the kernel's epilogue; an unquantized shard beside quantized ones is
+  multiplied as it is and concatenated, then ``out.add_(bias)``.  M = 0 returns an empty
+  [0, N] tensor.
 
 Layer attributes read (the plugin's): ``weight`` uint8 [N, K_bytes] with ``shard_id`` and
 ``shard_offset_map`` {idx: (start, end, size)}; ``weight_type.weight_type`` and
@@ -94,14 +95,18 @@ class GGUFLinearMethod:
             self.process_weights_after_loading(layer)
             groups = layer.gguf_groups
         if "__all__" in groups:
-            out = ops.mul_mat_grouped(x, groups["__all__"][0])
+            return ops.mul_mat_grouped(x, groups["__all__"][0], bias)   # bias fused into the epilogue
         else:
             shard_id = getattr(layer.weight, "shard_id", None) or list(getattr(layer, "gguf_shards", {}) or {})
             fallback = layer.weight_type.weight_type
             shard_types = getattr(layer.weight_type, "shard_weight_type", {}) or {}
             gguf_shards = getattr(layer, "gguf_shards", None)
+            order = _ordered_shard_ids(shard_id)
+            if len(groups) == 1 and set(next(iter(groups.values()))[1]) == set(order):
+                # every shard is in the one grouped run: one launch, bias fused
+                return ops.mul_mat_grouped(x, next(iter(groups.values()))[0], bias)
             result, done = [], set()
-            for idx in _ordered_shard_ids(shard_id):
+            for idx in order:
                 if idx in done:
                     continue
                 if idx in groups:

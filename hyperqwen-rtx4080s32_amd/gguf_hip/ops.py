@@ -238,7 +238,7 @@ def _pick_plan(plans: list[int], M: int) -> int:
 
 
 def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
-                  n_total: int, workspace: torch.Tensor) -> torch.Tensor:
+                  n_total: int, workspace: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
     M = int(x.shape[0])
     out = torch.empty((M, n_total), dtype=torch.bfloat16, device=x.device)
     if M == 0:
@@ -247,6 +247,7 @@ def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tenso
     info = GqkPlanInfo.from_tuple(plans[i * _NPLAN:(i + 1) * _NPLAN])
     check(lib.gqk_linear(ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(descs[i].data_ptr()), ctypes.byref(info),
                          ctypes.c_void_p(x.data_ptr()), x.stride(0), M, ctypes.c_void_p(out.data_ptr()), out.stride(0),
+                         ctypes.c_void_p(bias.data_ptr() if bias is not None else None),
                          ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
                          _stream(x.device)),
           "fused_mul_mat_gguf_grouped")
@@ -255,14 +256,15 @@ def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tenso
 
 @torch.library.custom_op("gguf_hip::fused_mul_mat_gguf_grouped", mutates_args=("workspace",))
 def fused_mul_mat_gguf_grouped(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
-                               n_total: int, workspace: torch.Tensor) -> torch.Tensor:
+                               n_total: int, workspace: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """x bf16 [M, K] -> bf16 [M, n_total]: one launch over a grouped layer's shards (columns in
-    shard order).  workspace: the layer's split-K counters and partials."""
-    return _grouped_impl(x, packed, descs, plans, n_total, workspace)
+    shard order).  workspace: the layer's split-K counters and partials.  bias: None or bf16
+    [n_total], added in the kernel's epilogue before the one rounding to bf16."""
+    return _grouped_impl(x, packed, descs, plans, n_total, workspace, bias)
 
 
 @fused_mul_mat_gguf_grouped.register_fake
-def _(x, packed, descs, plans, n_total, workspace):
+def _(x, packed, descs, plans, n_total, workspace, bias=None):
     return torch.empty((x.shape[0], n_total), dtype=torch.bfloat16, device=x.device)
 
 
@@ -280,10 +282,11 @@ def _ensure_workspace(gl: GroupedLayer, M: int) -> None:
         gl.workspace = torch.zeros((need + 3) // 4, dtype=torch.int32, device=gl.packed.device)
 
 
-def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer) -> torch.Tensor:
-    """y = x @ W^T for a prepared grouped layer, in x's dtype.  The kernels take bf16
+def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ W^T (+ bias) for a prepared grouped layer, in x's dtype.  The kernels take bf16
     activations; other floating dtypes are rounded to bf16 on the way in and the bf16 result
-    is cast back."""
+    is cast back.  A bf16 bias [n_total] is fused into the kernel's epilogue; a bias of another
+    dtype is added afterwards in that dtype (as the reference's out.add_(bias))."""
     _require_gpu(x, "mul_mat_grouped")
     if x.dim() != 2 or x.shape[1] != gl.K:
         raise ValueError(f"mul_mat_grouped: x {tuple(x.shape)} does not match K={gl.K}")
@@ -291,8 +294,17 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer) -> torch.Tensor:
     if xb.stride(1) != 1 or xb.stride(0) % 8 or xb.data_ptr() % 16:
         xb = xb.contiguous()
     _ensure_workspace(gl, int(xb.shape[0]))
-    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace)
-    return y if x.dtype == torch.bfloat16 else y.to(x.dtype)
+    fused = None
+    if bias is not None:
+        if bias.shape != (gl.n_total,) or bias.device != x.device:
+            raise ValueError(f"mul_mat_grouped: bias {tuple(bias.shape)} on {bias.device}, expected ({gl.n_total},)")
+        if bias.dtype == torch.bfloat16:
+            fused = bias.contiguous()
+    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace, fused)
+    y = y if x.dtype == torch.bfloat16 else y.to(x.dtype)
+    if bias is not None and fused is None:
+        y.add_(bias)
+    return y
 
 
 def fused_mul_mat_gguf(x: torch.Tensor, qweight: torch.Tensor, qweight_type: int) -> torch.Tensor:

@@ -104,8 +104,10 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
  * partial tiles, which depends on M and on the current device's CU count.  Replaces the reference's transient split-K partials (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
 int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
 
-/* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T over the grouped layer's shards (columns in shard
- * order), on `stream`.  desc_dev: the plan's descriptor table in device memory.  workspace: at
+/* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T (+ bias) over the grouped layer's shards (columns in
+ * shard order), on `stream`.  bias: NULL or bf16 [info->n_total] device memory, added in fp32
+ * before the single rounding to bf16 (the reference adds it afterwards with out.add_(bias),
+ * gguf-plugin/patches/gguf-tiles-grouped.patch:167-168).  desc_dev: the plan's descriptor table in device memory.  workspace: at
  * least gqk_linear_workspace_bytes(info, M) bytes of 256-byte aligned device memory (NULL when
  * that is 0) holding arrival counters (first) and fp32 partials; it must be zero-filled before
  * its first use, every launch leaves the counters at zero again, and launches sharing one
@@ -113,7 +115,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
-               int M, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes, void* stream);
+               int M, void* y, int64_t ldy, const void* bias, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- GGUF v3 files: the load path ----------------------------------------------------------
  * The reference's tensors come from vLLM's GGUF loader (gguf-py 0.17.1 GGUFReader,

@@ -168,6 +168,32 @@ def test_linear_method_mixed_and_single(dev):
         assert G.rel_err(method.apply(layer2, x).float().cpu().numpy(), _ref(x, wf2)) < TOL
 
 
+def test_fused_bias(dev):
+    """A bf16 bias is added in the kernels' epilogue (direct GEMV store, split-K fixup, GEMM and
+    stream-K fixup): a zero bias changes no bit, a random one matches oracle + bias; an fp32 bias
+    is added afterwards."""
+    import gguf_hip
+
+    rng = np.random.default_rng(12)
+    n, K = 1000, 2048
+    raw = G.make_weights(rng, n, K, G.Q4_K)
+    wf = G.dequantize(raw, G.Q4_K)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K])
+    zero = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    bias = (torch.randn(n, device=dev) * 4).to(torch.bfloat16)
+    for M in (1, 8, 16, 40, 100, 300):
+        x = _x(M, K, 6000 + M, dev)
+        y0 = gguf_hip.mul_mat_grouped(x, gl)
+        assert torch.equal(gguf_hip.mul_mat_grouped(x, gl, zero), y0), M
+        yb = gguf_hip.mul_mat_grouped(x, gl, bias).float().cpu().numpy()
+        ref = _ref(x, wf) + bias.float().cpu().numpy()[None]
+        assert G.rel_err(yb, ref) < TOL, M
+        y32 = gguf_hip.mul_mat_grouped(x, gl, bias.float())
+        assert torch.equal(y32, y0.add_(bias.float())), M
+    with pytest.raises(ValueError):
+        gguf_hip.mul_mat_grouped(_x(2, K, 1, dev), gl, bias[:10])
+
+
 def test_raw_rows_op_and_errors(dev):
     import gguf_hip
 
