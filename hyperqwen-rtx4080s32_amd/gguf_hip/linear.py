@@ -7,12 +7,13 @@ it (the plugin itself is not vendored):
   ``gguf-plugin/patches/gguf-tiles-grouped.patch:84-115``) become ``process_weights_after_loading``:
   every shard (or the whole weight of a single-type layer) is repacked to the tile layout, the
   run of shards is packed into one buffer with its launch plans, and the raw rows are freed.
-  All eleven types are tile types here, so a merged layer is always one run (one launch).
+  All eleven quantized types are tile types here, so a merged layer of them is one run (one
+  launch); an unquantized shard between them splits it into runs.
 * ``apply(layer, x, bias)`` (``gguf-plugin/patches/gguf-tiles-grouped.patch:131-171``,
   ``gguf-plugin/patches/gguf-iq3s-tiles.patch:98-136``): same-type or grouped -> one op, with
-  a bf16 bias fused into the kernel's epilogue; an unquantized shard beside quantized ones is
-  multiplied as it is and concatenated, then ``out.add_(bias)``.  M = 0 returns an empty
-  [0, N] tensor.
+  a bf16 bias fused into the kernel's epilogue; a shard of a type without a kernel here (an
+  unquantized one) splits the layer into runs, and each run and each such shard writes its
+  own column slice of one output, then ``out.add_(bias)``.  M = 0 returns an empty [0, N] tensor.
 
 Layer attributes read (the plugin's): ``weight`` uint8 [N, K_bytes] with ``shard_id`` and
 ``shard_offset_map`` {idx: (start, end, size)}; ``weight_type.weight_type`` and
@@ -65,13 +66,25 @@ class GGUFLinearMethod:
                 raws["__all__"], rows["__all__"], types["__all__"] = w, w.shape[0], wt
             else:
                 order = []
-        run = [i for i in order if i in raws]
+        # runs of consecutive shards with a kernel here (a shard of another type between them
+        # stays on its own path), as the reference's _create_groups
+        # (gguf-plugin/patches/gguf-tiles-grouped.patch:84-115)
+        runs, cur = [], []
+        for i in order:
+            if i in raws:
+                cur.append(i)
+            elif cur:
+                runs.append(cur)
+                cur = []
+        if cur:
+            runs.append(cur)
         groups = {}
-        if run:
-            K = {ops.quant_shape(types[i], rows[i], raws[i].shape[1])[1] for i in run}
+        if runs:
+            K = {ops.quant_shape(types[i], rows[i], raws[i].shape[1])[1] for r in runs for i in r}
             if len(K) != 1:
                 raise ValueError(f"process_weights_after_loading: shards with different K {sorted(K)}")
             K = K.pop()
+        for run in runs:
             for i in run:
                 tiles[i] = ops.repack_tiles(raws[i], rows[i], types[i])
             gl = ops.prepare_grouped_layer([tiles[i] for i in run], [rows[i] for i in run], [types[i] for i in run], K,
@@ -105,14 +118,14 @@ class GGUFLinearMethod:
             if len(groups) == 1 and set(next(iter(groups.values()))[1]) == set(order):
                 # every shard is in the one grouped run: one launch, bias fused
                 return ops.mul_mat_grouped(x, next(iter(groups.values()))[0], bias)
-            result, done = [], set()
-            for idx in order:
-                if idx in done:
-                    continue
+            # the pieces in shard order: grouped runs, and shards on their own path
+            pieces, i = [], 0
+            while i < len(order):
+                idx = order[i]
                 if idx in groups:
                     gl, run = groups[idx]
-                    result.append(ops.mul_mat_grouped(x, gl))
-                    done.update(run)
+                    pieces.append((gl.n_total, gl, None, None))
+                    i += len(run)
                     continue
                 wt = shard_types.get(idx, fallback)
                 if gguf_shards is not None:
@@ -120,8 +133,22 @@ class GGUFLinearMethod:
                 else:
                     start, end, size = layer.weight.shard_offset_map[idx]
                     shard = layer.weight[start:end, :size]
-                result.append(ops.fused_mul_mat_gguf(x, shard, wt))
-            out = result[0] if len(result) == 1 else torch.cat(result, dim=1)
+                pieces.append((shard.shape[0], None, shard, wt))
+                i += 1
+            if x.dtype == torch.bfloat16:
+                # every piece writes its own column slice of one output (no concatenation)
+                out = torch.empty((x.shape[0], sum(p[0] for p in pieces)), dtype=x.dtype, device=x.device)
+                c = 0
+                for n, gl, shard, wt in pieces:
+                    if gl is not None:
+                        ops.mul_mat_grouped(x, gl, out=out[:, c:c + n])
+                    else:
+                        out[:, c:c + n] = ops.fused_mul_mat_gguf(x, shard, wt)
+                    c += n
+            else:
+                result = [ops.mul_mat_grouped(x, gl) if gl is not None else ops.fused_mul_mat_gguf(x, shard, wt)
+                          for n, gl, shard, wt in pieces]
+                out = result[0] if len(result) == 1 else torch.cat(result, dim=1)
         if bias is not None:
             out.add_(bias)
         return out

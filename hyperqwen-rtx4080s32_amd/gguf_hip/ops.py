@@ -237,12 +237,11 @@ def _pick_plan(plans: list[int], M: int) -> int:
     return len(GEMV_BUCKETS) + len(GEMM_PLAN_M) - 1
 
 
-def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
-                  n_total: int, workspace: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+def _grouped_into(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
+                  workspace: torch.Tensor, bias: torch.Tensor | None, out: torch.Tensor) -> None:
     M = int(x.shape[0])
-    out = torch.empty((M, n_total), dtype=torch.bfloat16, device=x.device)
     if M == 0:
-        return out
+        return
     i = _pick_plan(plans, M)
     info = GqkPlanInfo.from_tuple(plans[i * _NPLAN:(i + 1) * _NPLAN])
     check(lib.gqk_linear(ctypes.c_void_p(packed.data_ptr()), ctypes.c_void_p(descs[i].data_ptr()), ctypes.byref(info),
@@ -251,6 +250,12 @@ def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tenso
                          ctypes.c_void_p(workspace.data_ptr()), workspace.numel() * workspace.element_size(),
                          _stream(x.device)),
           "fused_mul_mat_gguf_grouped")
+
+
+def _grouped_impl(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
+                  n_total: int, workspace: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    out = torch.empty((int(x.shape[0]), n_total), dtype=torch.bfloat16, device=x.device)
+    _grouped_into(x, packed, descs, plans, workspace, bias, out)
     return out
 
 
@@ -268,6 +273,14 @@ def _(x, packed, descs, plans, n_total, workspace, bias=None):
     return torch.empty((x.shape[0], n_total), dtype=torch.bfloat16, device=x.device)
 
 
+@torch.library.custom_op("gguf_hip::fused_mul_mat_gguf_grouped_out", mutates_args=("workspace", "out"))
+def fused_mul_mat_gguf_grouped_out(x: torch.Tensor, packed: torch.Tensor, descs: list[torch.Tensor], plans: list[int],
+                                   workspace: torch.Tensor, out: torch.Tensor, bias: torch.Tensor | None = None) -> None:
+    """As fused_mul_mat_gguf_grouped, writing into `out` (bf16 [M, n_total], unit column stride:
+    e.g. the column slice of a wider layer output that this run's shards own)."""
+    _grouped_into(x, packed, descs, plans, workspace, bias, out)
+
+
 def _ensure_workspace(gl: GroupedLayer, M: int) -> None:
     """Grow the layer's workspace (zero-filled, as the counters need) to what the plan serving M
     rows needs.  GEMV plans are covered at preparation; the large-M GEMM's stream-K partials
@@ -282,11 +295,14 @@ def _ensure_workspace(gl: GroupedLayer, M: int) -> None:
         gl.workspace = torch.zeros((need + 3) // 4, dtype=torch.int32, device=gl.packed.device)
 
 
-def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None = None) -> torch.Tensor:
+def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ W^T (+ bias) for a prepared grouped layer, in x's dtype.  The kernels take bf16
     activations; other floating dtypes are rounded to bf16 on the way in and the bf16 result
     is cast back.  A bf16 bias [n_total] is fused into the kernel's epilogue; a bias of another
-    dtype is added afterwards in that dtype (as the reference's out.add_(bias))."""
+    dtype is added afterwards in that dtype (as the reference's out.add_(bias)).  out: a bf16
+    [M, n_total] view with unit column stride (a column slice of a wider output) to write
+    into, for bf16 x; it is returned."""
     _require_gpu(x, "mul_mat_grouped")
     if x.dim() != 2 or x.shape[1] != gl.K:
         raise ValueError(f"mul_mat_grouped: x {tuple(x.shape)} does not match K={gl.K}")
@@ -300,6 +316,15 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
             raise ValueError(f"mul_mat_grouped: bias {tuple(bias.shape)} on {bias.device}, expected ({gl.n_total},)")
         if bias.dtype == torch.bfloat16:
             fused = bias.contiguous()
+    if out is not None:
+        if (x.dtype != torch.bfloat16 or out.dtype != torch.bfloat16 or out.shape != (xb.shape[0], gl.n_total)
+                or out.device != x.device or (out.numel() and out.stride(1) != 1)):
+            raise ValueError(f"mul_mat_grouped: out must be a bf16 [{xb.shape[0]}, {gl.n_total}] view with unit "
+                             f"column stride on {x.device}, for bf16 x")
+        fused_mul_mat_gguf_grouped_out(xb, gl.packed, gl.descs, gl.plans, gl.workspace, out, fused)
+        if bias is not None and fused is None:
+            out.add_(bias)
+        return out
     y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace, fused)
     y = y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     if bias is not None and fused is None:
@@ -312,7 +337,7 @@ def fused_mul_mat_gguf(x: torch.Tensor, qweight: torch.Tensor, qweight_type: int
     gguf-plugin/patches/gguf-prefill-dispatch.patch:9-50): y = x @ W^T.  Unprepared raw rows are
     repacked for this call (the loader's prepare step does it once instead)."""
     if qweight_type in UNQUANTIZED_TYPES:
-        return x @ qweight.T
+        return x @ (qweight if qweight.dtype == x.dtype else qweight.to(x.dtype)).T
     if qweight_type not in GGUF_TYPES:
         raise NotImplementedError(f"Unsupported GGUF quantization type: {qweight_type}")
     n = qweight.shape[0]

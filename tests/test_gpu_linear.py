@@ -168,6 +168,43 @@ def test_linear_method_mixed_and_single(dev):
         assert G.rel_err(method.apply(layer2, x).float().cpu().numpy(), _ref(x, wf2)) < TOL
 
 
+def test_linear_method_unquantized_shard_splits_runs(dev):
+    """A merged qkv layer whose k shard is unquantized (F16): the runs are [q] and [v] (as the
+    reference's _create_groups), every piece lands in its own output columns in q, k, v order,
+    for bf16 x (column slices of one output) and fp32 x (concatenation)."""
+    import gguf_hip
+
+    rng = np.random.default_rng(13)
+    K = 512
+    rq, rv = G.make_weights(rng, 128, K, G.Q4_K), G.make_weights(rng, 64, K, G.Q6_K)
+    wk = (rng.normal(size=(64, K)) * 0.02).astype(np.float16)
+    layer = _Layer()
+    layer.weight = torch.nn.Parameter(torch.empty(0, dtype=torch.uint8, device=dev), requires_grad=False)
+    layer.weight.shard_id = ["q", "k", "v"]
+    layer.weight_type = _WT(G.Q4_K, {"q": G.Q4_K, "k": 1, "v": G.Q6_K})
+    layer.gguf_shards = {"q": torch.from_numpy(rq).to(dev), "k": torch.from_numpy(wk).to(dev),
+                         "v": torch.from_numpy(rv).to(dev)}
+    method = gguf_hip.GGUFLinearMethod()
+    method.process_weights_after_loading(layer)
+    assert {k: v[1] for k, v in layer.gguf_groups.items()} == {"q": ["q"], "v": ["v"]}
+    wf = np.concatenate([G.dequantize(rq, G.Q4_K), wk.astype(np.float32), G.dequantize(rv, G.Q6_K)])
+    bias = torch.randn(256, device=dev).to(torch.bfloat16)
+    for M in (1, 8, 40):
+        x = _x(M, K, 7000 + M, dev)
+        y = method.apply(layer, x, bias)
+        ref = _ref(x, wf) + bias.float().cpu().numpy()[None]
+        assert y.shape == (M, 256) and G.rel_err(y.float().cpu().numpy(), ref) < TOL, M
+        y32 = method.apply(layer, x.float())
+        assert y32.dtype == torch.float32 and G.rel_err(y32.cpu().numpy(), _ref(x, wf)) < TOL, M
+    # the out= form writes exactly its column slice
+    gl = layer.gguf_groups["v"][0]
+    x = _x(5, K, 1, dev)
+    big = torch.full((5, 100), 7.0, dtype=torch.bfloat16, device=dev)
+    gguf_hip.mul_mat_grouped(x, gl, out=big[:, 20:84])
+    assert torch.equal(big[:, 20:84], gguf_hip.mul_mat_grouped(x, gl))
+    assert bool((big[:, :20] == 7).all()) and bool((big[:, 84:] == 7).all())
+
+
 def test_fused_bias(dev):
     """A bf16 bias is added in the kernels' epilogue (direct GEMV store, split-K fixup, GEMM and
     stream-K fixup): a zero bias changes no bit, a random one matches oracle + bias; an fp32 bias
