@@ -106,6 +106,7 @@ static int repack_common(const void* W, int64_t stride, int type, int64_t n, int
   if (n < 0 || K < 0 || K % 256 != 0) return fail(GQK_ERR_SHAPE, "repack: K=%lld is not a multiple of 256", (long long)K);
   if (n == 0 || K == 0) return GQK_OK;
   if (!W || !tiles) return fail(GQK_ERR_ARG, "repack: null pointer");
+  if ((uintptr_t)tiles & 15) return fail(GQK_ERR_SHAPE, "repack: tiles must be 16-byte aligned");
   if (stride < K / 256 * t->rec)
     return fail(GQK_ERR_SHAPE, "repack: row stride %lld < row bytes %lld", (long long)stride, (long long)(K / 256 * t->rec));
   int rc = gqk::launch_repack(type, W, stride, n, K, tiles, to_tiles, (hipStream_t)stream);

@@ -224,48 +224,126 @@ int launch_dequant(int type, const void* W, int64_t stride, int64_t n, int64_t K
 }
 
 // ---------------------------------------------------------------------------------------------
-// Repack raw rows <-> tiles.  One thread per (tile row, super-block): the record's bytes are
-// moved plane by plane; rows past n are written as zeros (repack) or skipped (unrepack).
+// Repack raw rows <-> tiles.  One workgroup per chunk (tile t, super-block kb): 64 rows x REC bytes.
+// Repack stages the chunk's 64 raw records in LDS (2-byte loads along each row when the rows are
+// 2-byte aligned, REC being even) and writes the chunk plane-major with 16-byte stores; unrepack
+// loads the chunk with 16-byte loads, scatters it into the 64 raw records in LDS and writes them
+// back row by row.  Rows past n are zeros in the tiles (repack) and are not written (unrepack).
+// Each byte crosses HBM once in each direction.  The plane table is a compile-time constant per
+// type, so the index arithmetic folds to shifts and multiplies by constants.
 
-struct PlaneArgs {
-  int nplanes;
-  int size[GQK_MAX_PLANES];
-  int nseg[GQK_MAX_PLANES];
-  int seg_off[GQK_MAX_PLANES];
-  int seg_len[GQK_MAX_PLANES];
-  int seg_stride[GQK_MAX_PLANES];
-};
+// raw byte of byte j of plane p (segments of equal length concatenated)
+template <int T, int P>
+__device__ __forceinline__ int raw_of(int j) {
+  constexpr gqk_plane pl = gqk_planes<T>::v.planes[P];
+  return pl.seg_off + (j / pl.seg_len) * pl.seg_stride + j % pl.seg_len;
+}
 
-template <bool TO_TILES>
+template <int T, int P>
+__device__ __forceinline__ constexpr int plane_off() {
+  int o = 0;
+  for (int p = 0; p < P; ++p) o += gqk_planes<T>::v.planes[p].size;
+  return o;
+}
+
+// visits the 16-byte words of plane P of a chunk: f(word index in the chunk, row of byte i, raw
+// byte of byte i) for i = 0..15 through g(i) -> (r, b)
+template <int T, int P, class F>
+__device__ __forceinline__ void plane_words(int tid, F&& f) {
+  constexpr gqk_plane pl = gqk_planes<T>::v.planes[P];
+  constexpr int W = gqk_col_width(pl.size), poff = plane_off<T, P>();
+  for (int w = tid; w < 4 * pl.size; w += 256) {     // 64 rows * size bytes / 16
+    const int x = 16 * w, col = x / (64 * W), rem = x % (64 * W);
+    f(4 * poff + w, [&](int i, int& r, int& b) {
+      r = (rem + i) / W;
+      b = raw_of<T, P>(col * W + (rem + i) % W);
+    });
+  }
+}
+
+template <int T, int P = 0, class F>
+__device__ __forceinline__ void every_plane_word(int tid, F&& f) {
+  if constexpr (P < gqk_planes<T>::v.nplanes) {
+    plane_words<T, P>(tid, f);
+    every_plane_word<T, P + 1>(tid, f);
+  }
+}
+
+template <int T, bool TO_TILES, bool WIDE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
-                                                     int64_t stride, int64_t n, int64_t nb, int rec, PlaneArgs pa) {
-  int64_t ntiles = (n + 63) / 64;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= ntiles * 64 * nb) return;
-  // i = ((tile * nb) + kb) * 64 + r: consecutive threads take consecutive rows of one chunk
-  int r = (int)(i % 64);
-  int64_t chunk = i / 64;
-  int64_t kb = chunk % nb, tile = chunk / nb;
-  int64_t row = tile * 64 + r;
-  uint8_t* tbase = (uint8_t*)(TO_TILES ? dst : src) + chunk * 64 * rec;
-  bool valid = row < n;
-  const uint8_t* rrec = (TO_TILES ? src : dst) + row * stride + kb * rec;
-  int poff = 0;
-  for (int p = 0; p < pa.nplanes; ++p) {
-    const int W = gqk_col_width(pa.size[p]);
-    uint8_t* tp = tbase + 64 * poff + r * W;     // byte j of the row: tp + (j / W) * 64 * W + j % W
-    int j = 0;
-    for (int sgi = 0; sgi < pa.nseg[p]; ++sgi) {
-      int so = pa.seg_off[p] + sgi * pa.seg_stride[p];
-      for (int b = 0; b < pa.seg_len[p]; ++b, ++j) {
-        uint8_t* tj = tp + (j / W) * 64 * W + j % W;
-        if (TO_TILES)
-          *tj = valid ? rrec[so + b] : (uint8_t)0;
-        else if (valid)
-          ((uint8_t*)rrec)[so + b] = *tj;
+                                                     int64_t stride, int64_t n, int64_t nb) {
+  constexpr gqk_type_c ty = gqk_planes<T>::v;
+  constexpr int REC = ty.rec, CB = 64 * REC;          // chunk bytes (a multiple of 64)
+  __shared__ __attribute__((aligned(16))) uint8_t raw[CB + 16];   // the 64 raw records, [row][REC]
+  const int tid = threadIdx.x;
+  const int64_t chunk = blockIdx.x, kb = chunk % nb, tile = chunk / nb;
+  const int64_t row0 = tile * 64;
+  if (TO_TILES) {
+    const uint8_t* rows = src + row0 * stride + kb * REC;
+    if (WIDE) {
+      for (int i = tid; i < CB / 2; i += 256) {
+        const int r = i / (REC / 2), h = i % (REC / 2);
+        const uint16_t v = row0 + r < n ? *(const uint16_t*)(rows + r * stride + 2 * h) : (uint16_t)0;
+        *(uint16_t*)(raw + r * REC + 2 * h) = v;
+      }
+    } else {
+      for (int i = tid; i < CB; i += 256) {
+        const int r = i / REC, b = i % REC;
+        raw[i] = row0 + r < n ? rows[r * stride + b] : (uint8_t)0;
       }
     }
-    poff += pa.size[p];
+    __syncthreads();
+    uint4* out = (uint4*)(dst + chunk * CB);
+    auto gather = [&](int wi, auto&& at) {
+      uint32_t v[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int r, b;
+        at(i, r, b);
+        v[i >> 2] |= (uint32_t)raw[r * REC + b] << (8 * (i & 3));
+      }
+      out[wi] = make_uint4(v[0], v[1], v[2], v[3]);
+    };
+    every_plane_word<T>(tid, gather);
+  } else {
+    const uint4* in = (const uint4*)(src + chunk * CB);
+    auto scatter = [&](int wi, auto&& at) {
+      const uint4 q = in[wi];
+      const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        int r, b;
+        at(i, r, b);
+        raw[r * REC + b] = (uint8_t)(v[i >> 2] >> (8 * (i & 3)));
+      }
+    };
+    every_plane_word<T>(tid, scatter);
+    __syncthreads();
+    uint8_t* rows = dst + row0 * stride + kb * REC;
+    if (WIDE) {
+      for (int i = tid; i < CB / 2; i += 256) {
+        const int r = i / (REC / 2), h = i % (REC / 2);
+        if (row0 + r < n) *(uint16_t*)(rows + r * stride + 2 * h) = *(const uint16_t*)(raw + r * REC + 2 * h);
+      }
+    } else {
+      for (int i = tid; i < CB; i += 256) {
+        const int r = i / REC, b = i % REC;
+        if (row0 + r < n) rows[r * stride + b] = raw[i];
+      }
+    }
+  }
+}
+
+template <int T>
+static void launch_repack_t(bool to_tiles, bool wide, dim3 grid, hipStream_t st, const uint8_t* s, uint8_t* d,
+                            int64_t stride, int64_t n, int64_t nb) {
+  const dim3 block(256);
+  if (to_tiles) {
+    if (wide) hipLaunchKernelGGL((repack_kernel<T, true, true>), grid, block, 0, st, s, d, stride, n, nb);
+    else hipLaunchKernelGGL((repack_kernel<T, true, false>), grid, block, 0, st, s, d, stride, n, nb);
+  } else {
+    if (wide) hipLaunchKernelGGL((repack_kernel<T, false, true>), grid, block, 0, st, s, d, stride, n, nb);
+    else hipLaunchKernelGGL((repack_kernel<T, false, false>), grid, block, 0, st, s, d, stride, n, nb);
   }
 }
 
@@ -273,24 +351,22 @@ int launch_repack(int type, const void* W, int64_t stride, int64_t n, int64_t K,
                   hipStream_t st) {
   const gqk_type* t = gqk_type_get(type);
   if (!t) return GQK_ERR_TYPE;
-  PlaneArgs pa{};
-  pa.nplanes = t->nplanes;
-  for (int p = 0; p < t->nplanes; ++p) {
-    pa.size[p] = t->planes[p].size;
-    pa.nseg[p] = t->planes[p].nseg;
-    pa.seg_off[p] = t->planes[p].seg_off;
-    pa.seg_len[p] = t->planes[p].seg_len;
-    pa.seg_stride[p] = t->planes[p].seg_stride;
+  const int64_t nb = K / 256, ntiles = (n + 63) / 64;
+  const int64_t chunks = ntiles * nb;
+  if (chunks == 0) return GQK_OK;
+  if (chunks >= ((int64_t)1 << 31)) return GQK_ERR_SHAPE;
+  // 2-byte accesses along the raw rows when every row starts 2-byte aligned (every REC is even)
+  const bool wide = (t->rec % 2 == 0) && (stride % 2 == 0) && ((uintptr_t)W % 2 == 0);
+  const dim3 grid((unsigned)chunks);
+  const uint8_t* s = (const uint8_t*)(to_tiles ? W : tiles);
+  uint8_t* d = (uint8_t*)(to_tiles ? tiles : W);
+  switch (type) {
+#define C(T) case T: launch_repack_t<T>(to_tiles, wide, grid, st, s, d, stride, n, nb); return GQK_OK;
+    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
   }
-  int64_t nb = K / 256, ntiles = (n + 63) / 64;
-  int64_t total = ntiles * 64 * nb;
-  if (total == 0) return GQK_OK;
-  dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (to_tiles)
-    hipLaunchKernelGGL(repack_kernel<true>, grid, block, 0, st, (const uint8_t*)W, (uint8_t*)tiles, stride, n, nb, t->rec, pa);
-  else
-    hipLaunchKernelGGL(repack_kernel<false>, grid, block, 0, st, (const uint8_t*)tiles, (uint8_t*)W, stride, n, nb, t->rec, pa);
-  return GQK_OK;
+  return GQK_ERR_TYPE;
 }
 
 }  // namespace gqk

@@ -67,6 +67,17 @@ struct gqk_type {
   X(GQK_IQ3_S, 256, 110, 110, 5, {{64, 1, 2, 64, 0}, {32, 1, 74, 32, 0}, {8, 1, 66, 8, 0}, {4, 1, 106, 4, 0}, {2, 1, 0, 2, 0}}) \
   X(GQK_IQ4_XS, 256, 136, 136, 2, {{128, 1, 8, 128, 0}, {8, 1, 0, 8, 0}})
 
+// The same table as compile-time constants per type (device code)
+struct gqk_type_c {
+  int rec, nplanes;
+  gqk_plane planes[GQK_MAX_PLANES];
+};
+template <int T> struct gqk_planes;
+#define X(ID, BW, BB, REC, NP, ...) \
+  template <> struct gqk_planes<ID> { static constexpr gqk_type_c v = {REC, NP, __VA_ARGS__}; };
+GQK_TYPES_TABLE
+#undef X
+
 // Column width of a plane of `size` bytes per row: 16, or the largest power of two dividing it.
 __host__ __device__ constexpr int gqk_col_width(int size) {
   return size % 16 == 0 ? 16 : size % 8 == 0 ? 8 : size % 4 == 0 ? 4 : size % 2 == 0 ? 2 : 1;

@@ -94,6 +94,35 @@ def test_repack_layout_and_roundtrip(dev, wt):
     assert np.array_equal(w, G.dequantize(raw, wt))
 
 
+@pytest.mark.parametrize("wt", [G.Q4_0, G.Q6_K, G.IQ3_S], ids=lambda t: G.NAMES[t])
+def test_repack_odd_stride_rows(dev, wt):
+    """Rows at an odd byte stride inside a larger buffer (the byte-wide load path), 130 rows
+    (a partial last tile), and the C ABI's unrepack into rows at that stride."""
+    import ctypes
+
+    import gguf_hip
+    from gguf_hip._lib import lib
+
+    rng = np.random.default_rng(500 + wt)
+    n, K = 130, 512
+    raw = G.random_blocks(rng, n, K, wt)
+    rb = raw.shape[1]
+    big = np.zeros((n, rb + 3), np.uint8)
+    big[:, 1:1 + rb] = raw
+    Wbig = _to_dev(big, dev)
+    view = Wbig[:, 1:1 + rb]                                     # odd base, odd row stride
+    assert view.stride(0) % 2 == 1 and view.data_ptr() % 2 == 1
+    tiles = gguf_hip.repack_tiles(view, n, wt)
+    _, _, rec, _ = gguf_hip.type_info(wt)
+    assert np.array_equal(tiles.cpu().numpy(), _np_repack(raw, wt, n, K, gguf_hip.type_planes(wt), rec))
+    out = torch.full((n, rb + 3), 0xAB, dtype=torch.uint8, device=dev)
+    rc = lib.gqk_unrepack(ctypes.c_void_p(tiles.data_ptr()), wt, n, K, ctypes.c_void_p(out.data_ptr() + 1),
+                          out.stride(0), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    assert rc == 0
+    o = out.cpu().numpy()
+    assert np.array_equal(o[:, 1:1 + rb], raw) and (o[:, 0] == 0xAB).all() and (o[:, 1 + rb:] == 0xAB).all()
+
+
 def test_repack_rejects_bad_k(dev):
     import gguf_hip
 
