@@ -179,8 +179,9 @@ template <> __device__ __forceinline__ _Float16 cvt_out<_Float16>(float v) {
   return (_Float16)v;
 }
 
-// One thread per (row, group of 32 weights).
-template <int T, typename O>
+// One thread per (row, group of 32 weights).  VEC: the output rows are 16-byte aligned, so the
+// 32 values go out as 16-byte stores (64 or 128 contiguous bytes per thread).
+template <int T, typename O, bool VEC>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ W, int64_t stride, int64_t n,
                                                       int64_t K, O* __restrict__ out, int64_t ldo, int rec) {
   int64_t ng = K / 32;
@@ -193,8 +194,20 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   float w[32];
   deq32<T>(recp, g, w);
   O* o = out + row * ldo + gg * 32;
+  if constexpr (VEC) {
+    constexpr int PER = 16 / sizeof(O);   // values per 16-byte store
+    uint4* ov = (uint4*)o;
 #pragma unroll
-  for (int j = 0; j < 32; ++j) o[j] = cvt_out<O>(w[j]);
+    for (int v = 0; v < 32 / PER; ++v) {
+      O c[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) c[j] = cvt_out<O>(w[v * PER + j]);
+      ov[v] = __builtin_bit_cast(uint4, c);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[j] = cvt_out<O>(w[j]);
+  }
 }
 
 template <int T>
@@ -203,12 +216,17 @@ static int launch_dequant_t(const void* W, int64_t stride, int64_t n, int64_t K,
   const int rec = gqk_layout<T>::REC;
   int64_t total = n * (K / 32);
   dim3 grid((unsigned)((total + 255) / 256)), block(256);
-  if (dtype == 0)
-    hipLaunchKernelGGL((dequant_kernel<T, float>), grid, block, 0, st, (const uint8_t*)W, stride, n, K, (float*)out, ldo, rec);
-  else if (dtype == 1)
-    hipLaunchKernelGGL((dequant_kernel<T, __bf16>), grid, block, 0, st, (const uint8_t*)W, stride, n, K, (__bf16*)out, ldo, rec);
-  else
-    hipLaunchKernelGGL((dequant_kernel<T, _Float16>), grid, block, 0, st, (const uint8_t*)W, stride, n, K, (_Float16*)out, ldo, rec);
+  const int esz = dtype == 0 ? 4 : 2;
+  const bool vec = ((uintptr_t)out % 16 == 0) && ((ldo * esz) % 16 == 0);
+#define L(O, V) hipLaunchKernelGGL((dequant_kernel<T, O, V>), grid, block, 0, st, (const uint8_t*)W, stride, n, K, (O*)out, ldo, rec)
+  if (dtype == 0) {
+    if (vec) L(float, true); else L(float, false);
+  } else if (dtype == 1) {
+    if (vec) L(__bf16, true); else L(__bf16, false);
+  } else {
+    if (vec) L(_Float16, true); else L(_Float16, false);
+  }
+#undef L
   return GQK_OK;
 }
 

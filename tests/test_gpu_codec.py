@@ -49,6 +49,32 @@ def test_dequantize_strided_rows_and_quantized_weights(dev, wt):
     assert np.array_equal(got.view(np.uint32), G.dequantize(raw, wt).view(np.uint32))
 
 
+@pytest.mark.parametrize("wt", [G.Q4_K, G.Q8_0, G.IQ3_S], ids=lambda t: G.NAMES[t])
+def test_dequantize_unaligned_output_rows(dev, wt):
+    """Output rows that are not 16-byte aligned (ld_out = K + 3) take the element-wise store
+    path; rows of a 16-byte aligned ld_out the vector path: both bit-exact."""
+    import ctypes
+
+    import gguf_hip
+    from gguf_hip._lib import lib
+
+    rng = np.random.default_rng(350 + wt)
+    n, K = 37, 512
+    raw = G.random_blocks(rng, n, K, wt)
+    ref = torch.from_numpy(G.dequantize(raw, wt))
+    W = _to_dev(raw, dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    for dt, code in ((torch.float32, 0), (torch.bfloat16, 1), (torch.float16, 2)):
+        for ld in (K + 3, K + 8):
+            out = torch.full((n, ld), 7, dtype=dt, device=dev)
+            rc = lib.gqk_dequantize(ctypes.c_void_p(W.data_ptr()), W.stride(0), wt, n, K, ctypes.c_void_p(out.data_ptr()),
+                                    ld, code, st)
+            assert rc == 0
+            o = out.cpu()
+            assert torch.equal(o[:, :K], ref.to(dt)), (dt, ld)
+            assert bool((o[:, K:] == 7).all()), (dt, ld)
+
+
 @pytest.mark.parametrize("wt", [G.Q4_0, G.Q5_0, G.Q8_0, G.IQ4_NL], ids=lambda t: G.NAMES[t])
 def test_dequantize_32_block_types_any_k(dev, wt):
     import gguf_hip
