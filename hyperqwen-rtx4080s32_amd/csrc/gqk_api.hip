@@ -169,6 +169,12 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   };
   int64_t tiles = 0;
   for (int i = 0; i < nshards; ++i) tiles += (shards[i].n + 63) / 64;
+  // One counter region for every plan of the layer (the GEMV's per-tile split-K counters, the
+  // GEMM's stream-K workgroups), so that one workspace serves every M: no plan's partials
+  // overlap another plan's counters.
+  const int64_t ctr_bytes = std::max(gqk_counter_bytes(tiles), gqk_counter_bytes(GQK_GEMM_MAX_WGS));
+  if (ctr_bytes >= ((int64_t)1 << 31)) return fail(GQK_ERR_SHAPE, "plan: %lld tiles", (long long)tiles);
+  pi.ctr_bytes = (int32_t)ctr_bytes;
   if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
@@ -179,6 +185,9 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
     // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
     // workgroup holds does K split across workgroups.  Every wave keeps >= 1 super-block.
+    // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
+    // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
+    // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
     const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWaves;
     const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
     const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
@@ -194,9 +203,9 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
           row(i, t0, 1, s * nb / split, (s + 1) * nb / split, (int)s, col0, ctr);
       col0 += shards[i].n;
     }
-    // workspace: tile arrival counters (zero before the first launch, left zero by each launch),
-    // then the fp32 partials [tile][split][64 rows][m_max tokens]
-    pi.workspace_bytes = split > 1 ? gqk_counter_bytes(tiles) + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
+    // workspace: the counter region (one arrival counter per tile; zero before the first launch,
+    // left zero by each launch), then the fp32 partials [tile][split][64 rows][m_max tokens]
+    pi.workspace_bytes = split > 1 ? ctr_bytes + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
     // 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens on
@@ -229,7 +238,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
   if (M <= 0) return 0;
   if (info->form == GQK_FORM_GEMV) return info->split > 1 ? info->workspace_bytes : 0;
   if (info->form == GQK_FORM_GEMM) {
-    const int64_t n = gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb);
+    const int64_t n = gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb, info->ctr_bytes);
     return n < 0 ? fail(GQK_ERR_HIP, "linear_workspace_bytes: no HIP device") : n;
   }
   return fail(GQK_ERR_FORM, "linear_workspace_bytes: unknown form %d", info->form);
@@ -255,7 +264,8 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     float* partials = nullptr;
     if (info->split > 1) {
       tiles = info->n_desc / info->split;   // one descriptor row per (tile, split)
-      const int64_t cb = gqk_counter_bytes(tiles);
+      const int64_t cb = info->ctr_bytes;
+      if (cb < gqk_counter_bytes(tiles)) return fail(GQK_ERR_FORM, "linear: counter region %lld bytes", (long long)cb);
       const int64_t need = cb + gqk_partial_bytes(tiles, info->split, 4 * info->g);
       if (!workspace || workspace_bytes < need)
         return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);
@@ -272,10 +282,12 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     if (M <= GQK_GEMV_MAX_M) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
     if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
     int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
-                              bias, info->bm, workspace, workspace_bytes, (hipStream_t)stream);
+                              bias, info->bm, info->ctr_bytes, workspace, workspace_bytes, (hipStream_t)stream);
     if (rc == GQK_ERR_SHAPE)
       return fail(rc, "linear: GEMM workspace %lld bytes < %lld (or not 256-byte aligned)", (long long)workspace_bytes,
-                  (long long)gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb));
+                  (long long)gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb, info->ctr_bytes));
+    if (rc == GQK_ERR_FORM)
+      return fail(rc, "linear: %d-byte counter region below the device's persistent GEMM workgroups", info->ctr_bytes);
     if (rc) return fail(rc, "linear: GEMM launch form bm=%d", info->bm);
     return check_launch("linear (GEMM)");
   }

@@ -752,26 +752,28 @@ static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb) {
   return std::max<int64_t>(1, std::min<int64_t>(G, R * 4 * nb));
 }
 
-int64_t gemm_workspace(int bm, int n_desc, int M, int nb) {
+// Workspace: ctr_bytes of counters (the plan's counter region: at least G ints), then the partial tiles.
+int64_t gemm_workspace(int bm, int n_desc, int M, int nb, int64_t ctr_bytes) {
   const int G = gb_workgroups(bm);
   if (G <= 0) return -1;
   const int64_t T = (int64_t)n_desc * ((M + bm - 1) / bm);
   const int64_t R = T % G;
   if (R == 0) return 0;
   const int64_t gsk = gb_stream_k_workgroups(G, R, nb);
-  return ((int64_t)G * 4 + 255) / 256 * 256 + (R + gsk - 1) * gb_slot_floats(bm) * 4;
+  return ctr_bytes + (R + gsk - 1) * gb_slot_floats(bm) * 4;
 }
 
 template <class GE>
 static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
-                     const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, const uint16_t* bias, void* ws,
-                     int64_t ws_bytes) {
+                     const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, const uint16_t* bias,
+                     int64_t ctr_bytes, void* ws, int64_t ws_bytes) {
   const int G = gb_workgroups(GE::BM);
   if (G <= 0) return GQK_ERR_HIP;
-  const int64_t need = gemm_workspace(GE::BM, n_desc, M, nb);
+  if ((int64_t)G * 4 > ctr_bytes || (ctr_bytes & 255)) return GQK_ERR_FORM;
+  const int64_t need = gemm_workspace(GE::BM, n_desc, M, nb, ctr_bytes);
   if (need > 0 && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255))) return GQK_ERR_SHAPE;
   int* ctr = (int*)ws;
-  float* part = need > 0 ? (float*)((char*)ws + ((int64_t)G * 4 + 255) / 256 * 256) : nullptr;
+  float* part = need > 0 ? (float*)((char*)ws + ctr_bytes) : nullptr;
   // G workgroups when there are at least G tiles; else the stream-K participants only
   const int64_t T = (int64_t)n_desc * ((M + GE::BM - 1) / GE::BM);
   const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb);
@@ -788,16 +790,16 @@ static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const 
 }
 
 int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int64_t K, void* y, int64_t ldy, const void* bias, int bm, void* ws, int64_t ws_bytes,
-                hipStream_t st) {
+                int M, int64_t K, void* y, int64_t ldy, const void* bias, int bm, int64_t ctr_bytes, void* ws,
+                int64_t ws_bytes, hipStream_t st) {
   const int nb = (int)(K / 256);
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
   switch (bm) {
-    case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
-    case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
-    case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ws, ws_bytes);
+    case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
+    case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
+    case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     default: return GQK_ERR_FORM;
   }
 }

@@ -35,7 +35,7 @@ class GqkShard(ctypes.Structure):
 class GqkPlanInfo(ctypes.Structure):
     _fields_ = [("form", ctypes.c_int32), ("m_max", ctypes.c_int32), ("g", ctypes.c_int32), ("bm", ctypes.c_int32),
                 ("split", ctypes.c_int32), ("n_desc", ctypes.c_int32), ("types_mask", ctypes.c_int32),
-                ("nb", ctypes.c_int32), ("nw", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("nb", ctypes.c_int32), ("nw", ctypes.c_int32), ("ctr_bytes", ctypes.c_int32),
                 ("n_total", ctypes.c_int64), ("workspace_bytes", ctypes.c_int64)]
 
     def as_tuple(self) -> tuple:

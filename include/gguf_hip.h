@@ -54,7 +54,8 @@ typedef struct gqk_plan_info {
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
   int32_t nb;         /* K / 256 */
   int32_t nw;         /* GEMV: waves per workgroup (they split the workgroup's k-range) */
-  int32_t reserved;
+  int32_t ctr_bytes;  /* bytes of arrival counters at the start of the workspace; the same in every
+                         plan of one layer, so one workspace serves all of them */
   int64_t n_total;    /* output columns: sum of the shards' rows */
   int64_t workspace_bytes; /* device workspace gqk_linear needs (any M <= m_max) */
 } gqk_plan_info;
@@ -109,9 +110,10 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
  * before the single rounding to bf16 (the reference adds it afterwards with out.add_(bias),
  * gguf-plugin/patches/gguf-tiles-grouped.patch:167-168).  desc_dev: the plan's descriptor table in device memory.  workspace: at
  * least gqk_linear_workspace_bytes(info, M) bytes of 256-byte aligned device memory (NULL when
- * that is 0) holding arrival counters (first) and fp32 partials; it must be zero-filled before
- * its first use, every launch leaves the counters at zero again, and launches sharing one
- * workspace must not overlap in time.  M must be <= info->m_max (and > 16 for a GEMM plan).  Replaces the grouped op
+ * that is 0) holding arrival counters (its first info->ctr_bytes bytes) and fp32 partials (after
+ * them); it must be zero-filled before its first use, every launch leaves the counters at zero
+ * again, one workspace serves every plan of one layer (any M: the counter region is the same in
+ * all of them), and launches sharing one workspace must not overlap in time.  M must be <= info->m_max (and > 16 for a GEMM plan).  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,

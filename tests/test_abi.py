@@ -88,7 +88,9 @@ def test_plan_gemv_balanced_split_partition():
         assert first[:, 6].tolist() == [(s + 1) * 20 // S for s in range(S)]
         assert first[:, 7].tolist() == list(range(S)) and (first[:, 11] == 0).all()
         assert sorted(set(d[:, 11].tolist())) == list(range(96))   # one arrival counter per tile
-        assert info.workspace_bytes == (512 + S * 4 * 6144 * 4 if S > 1 else 0)
+        # the counter region: one int per tile, at least the GEMM's 1024 workgroups, 256-byte rounded
+        assert info.ctr_bytes == 4096
+        assert info.workspace_bytes == (4096 + S * 4 * 6144 * 4 if S > 1 else 0)
     assert ops.plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
     info = ops.plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
     assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
@@ -105,6 +107,10 @@ def test_plan_descriptor_rows_mixed_layer():
     d = _rows(desc)
     assert info.types_mask == 0 and info.n_total == 370 and info.g == 2
     assert info.split == 1 and info.workspace_bytes == 0
+    # one counter region for every plan of a layer, so one workspace serves every M
+    for shards, k in (([(21, 70, 0), (12, 300, off2)], K), ([(12, 70000, 0)], 512)):
+        regions = {ops.plan(shards, k, m, t)[0].ctr_bytes for m in (1, 8, 16, 17, 100, 2048) for t in (0, 1, 4096)}
+        assert regions == {max(4096, ((sum((n + 63) // 64 for _, n, _ in shards) * 4 + 255) // 256) * 256)}
     # one workgroup per tile: IQ3_S 2 tiles (64 + 6 rows), Q4_K 5 tiles (4 x 64 + 44)
     assert d[:, 0].tolist() == [21, 21, 12, 12, 12, 12, 12]
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7

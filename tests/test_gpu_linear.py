@@ -85,7 +85,33 @@ def test_split_k_repeat_is_bit_identical(dev):
         for _ in range(30):
             assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y0)
     torch.cuda.synchronize()
-    assert int(gl.workspace[:((n + 63) // 64)].abs().sum()) == 0
+    assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
+
+
+def test_one_workspace_serves_every_form(dev):
+    """One layer workspace across the GEMV (split tiles) and the three GEMM forms (stream-K
+    partials) in an order where each form's partials would land on another form's counters if
+    the counter regions differed: every call matches the oracle and repeats bit-identically,
+    and the counters end at zero."""
+    import gguf_hip
+
+    rng = np.random.default_rng(12)
+    n, K = 900, 12 * 256
+    raw = G.random_blocks(rng, n, K, G.Q4_K)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K], target_wgs=2048)
+    wf = G.dequantize(raw, G.Q4_K)
+    first = {}
+    for M in (300, 1, 40, 100, 300, 8, 40, 1, 100):
+        x = _x(M, K, 9000 + M, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        if M not in first:
+            assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
+            first[M] = y
+        else:
+            assert torch.equal(y, first[M]), M
+    torch.cuda.synchronize()
+    info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[:gguf_hip.ops._NPLAN])
+    assert info.split > 1 and int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
 
 
 def test_mixed_layer_one_launch(dev):
