@@ -385,6 +385,8 @@ struct Geo {
   static_assert(BN * 2 == NT, "one thread per (weight row, part)");
   static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
 };
+// (x / weight prefetch depths of 2 / 2, 3 / 3 and 1 / 3 for the two smaller forms measured the
+// same as 1 / 2 within noise.)
 typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
 typedef Geo<128, 128, 2, 2, 1, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
 typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 17..64 tokens
@@ -746,10 +748,13 @@ static int gb_cus() {
 static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : 2); }
 static int gb_slot_floats(int bm) { return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : GeoSmall::SLOT; }
 
-// Stream-K workgroups for R remainder tiles of 4 nb steps: all G, or one per step when there are
-// fewer steps.  (Longer ranges, i.e. fewer contributors per tile, measured slower.)
+// Stream-K workgroups for R remainder tiles of S = 4 nb steps: at most G, at least 16 steps per
+// workgroup and at most 6 workgroups per tile.  The last contributor of a tile sums every other
+// one's partial slot in dependent device-scope round trips, so contributors cost more than the
+// steps they take over: measured on the 5120-row shards at M = 17..200, all G workgroups (13
+// per tile) took 33-110 us, 16 steps / <= 6 per tile 22-70 us; tile-rich shards keep all G.
 static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb) {
-  return std::max<int64_t>(1, std::min<int64_t>(G, R * 4 * nb));
+  return std::max<int64_t>(1, std::min<int64_t>({(int64_t)G, R * 4 * nb / 16, 6 * R}));
 }
 
 // Workspace: ctr_bytes of counters (the plan's counter region: at least G ints), then the partial tiles.

@@ -115,9 +115,11 @@ def test_one_workspace_serves_every_form(dev):
 
 
 def test_mixed_layer_one_launch(dev):
-    """A merged layer of three types in one grouped launch; with split 1 every shard's columns
-    are bit-identical to its own launch (the reference's mixed-layer identity,
-    gguf-plugin/test_gluon_kq_gpu.py:172-195)."""
+    """A merged layer of five types in one grouped launch.  GEMV (split 1): every shard's columns
+    are bit-identical to its own launch (the reference's mixed-layer identity at a fixed split,
+    gguf-plugin/test_gluon_kq_gpu.py:172-195).  GEMM: the stream-K k-ranges of a tile depend on
+    the launch's whole tile count, so a shard's fp32 partial sums may associate differently
+    alone: its columns match the oracle and stay within bf16 rounding of its own launch."""
     import gguf_hip
 
     rng = np.random.default_rng(7)
@@ -135,7 +137,15 @@ def test_mixed_layer_one_launch(dev):
         col = 0
         for s, (wt, n) in zip(singles, shards):
             ys = gguf_hip.mul_mat_grouped(x, s)
-            assert torch.equal(y[:, col:col + n], ys), (M, G.NAMES[wt])
+            if M <= 16:
+                assert torch.equal(y[:, col:col + n], ys), (M, G.NAMES[wt])
+            else:
+                a, b = y[:, col:col + n].float(), ys.float()
+                # the two fp32 sums differ by reassociation only (~1e-6 of the row's scale), so the
+                # bf16 results are at most one rounding step apart
+                rowmax = b.abs().amax(dim=1, keepdim=True)
+                bound = torch.maximum(a.abs(), b.abs()) * 2.0 ** -7 + 1e-4 * rowmax
+                assert ((a - b).abs() <= bound).all(), (M, G.NAMES[wt])
             col += n
 
 
