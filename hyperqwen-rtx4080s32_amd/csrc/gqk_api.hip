@@ -208,9 +208,9 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     pi.workspace_bytes = split > 1 ? ctr_bytes + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
-    // 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens on
-    // the GEMM outruns the GEMV's 4 x 4 x 4 MFMAs (one decode of each weight for up to 64 tokens).
-    pi.bm = M <= 64 ? 64 : M <= 128 ? 128 : 256;
+    // 32 / 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens
+    // on the GEMM outruns the GEMV's 4 x 4 x 4 MFMAs (one decode of each weight for up to 128 tokens).
+    pi.bm = M <= 32 ? 32 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
     pi.m_max = 1 << 30;
     pi.split = 1;
     const int64_t per = pi.bm == 256 ? 4 : 2;   // tiles per descriptor row

@@ -123,7 +123,7 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 // descriptor row of a grouped launch (int32 words)
 #define GQK_DESC_WORDS 16
 #define GQK_SPLIT_MAX 16   // split-K factor bound: the last workgroup loads every partial at once
-#define GQK_GEMM_MAX_WGS 1024   // persistent GEMM workgroups (two per CU) a launch may use: the counter region
+#define GQK_GEMM_MAX_WGS 1024   // persistent GEMM workgroups (up to three per CU) a launch may use: the counter region
 #ifndef GQK_GEMV_MAX_M
 #define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form; the GEMM above
 #endif

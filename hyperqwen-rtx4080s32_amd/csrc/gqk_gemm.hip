@@ -382,6 +382,7 @@ struct Geo {
   static constexpr int CH = MB * NB * 4;                          // 16-byte accumulator chunks per thread
   static constexpr int SLOT = BM * BN;                            // floats per partial slot
   static constexpr int LDS = 2 * (BM + BN) * GB_LD * 2;           // double-buffered x and weights
+  static constexpr int WPE = BM <= 32 ? 3 : 2;                    // waves per SIMD kept resident
   static_assert(BN * 2 == NT, "one thread per (weight row, part)");
   static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
 };
@@ -389,7 +390,8 @@ struct Geo {
 // same as 1 / 2 within noise.)
 typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
 typedef Geo<128, 128, 2, 2, 1, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
-typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 17..64 tokens
+typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 33..64 tokens
+typedef Geo<32, 128, 1, 4, 1, 2> GeoTiny;    // 17..32 tokens: 4 waves side by side, three workgroups per CU
 
 template <int S, class V>
 __device__ __forceinline__ V& pick(V& a, V& b, V& c) {
@@ -651,7 +653,7 @@ __device__ __forceinline__ void gb_map(int i, int n_desc, int nmb, int& d, int& 
 // dealt round robin; the remaining R tiles' k-steps split evenly over gsk workgroups (stream-K,
 // gb_stream_k_workgroups), tiles shared by several workgroups combined through partial slots.
 template <class GE, int ONLY>
-__global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(2))) void gemm_sk_kernel(const uint8_t* __restrict__ packed,
+__global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(GE::WPE))) void gemm_sk_kernel(const uint8_t* __restrict__ packed,
                                                           const int32_t* __restrict__ desc, int n_desc,
                                                           const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                           uint16_t* __restrict__ y, int64_t ldy,
@@ -745,8 +747,10 @@ static int gb_cus() {
 }
 
 // persistent workgroups of a form: every one resident (the 256 form takes a whole CU's LDS)
-static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : 2); }
-static int gb_slot_floats(int bm) { return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : GeoSmall::SLOT; }
+static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : bm == 32 ? 3 : 2); }
+static int gb_slot_floats(int bm) {
+  return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : bm == 64 ? GeoSmall::SLOT : GeoTiny::SLOT;
+}
 
 // Stream-K workgroups for R remainder tiles of S = 4 nb steps: at most G, at least 16 steps per
 // workgroup and at most 6 workgroups per tile.  The last contributor of a tile sums every other
@@ -805,6 +809,7 @@ int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int type
     case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
+    case 32: return launch_sk<GeoTiny>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     default: return GQK_ERR_FORM;
   }
 }

@@ -127,6 +127,7 @@ def test_plan_descriptor_rows_mixed_layer():
     assert g[:, 4].tolist() == [2, 4, 1] and g[:, 9].tolist() == [70, 256, 44]
     assert g[:, 8].tolist() == [0, 70, 326]
     assert ops.plan([(21, 70, 0), (12, 300, off2)], K, 40)[0].bm == 64
+    assert ops.plan([(21, 70, 0), (12, 300, off2)], K, 20)[0].bm == 32
 
 
 def test_plan_buckets():
@@ -136,7 +137,8 @@ def test_plan_buckets():
         info, _ = ops.plan([(12, 512, 0)], 512, M)
         assert info.form == 1 and info.g == g and info.m_max == 4 * g
     assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 16) == 2
-    assert ops._pick_plan([], 17) == 3 and ops._pick_plan([], 64) == 3 and ops._pick_plan([], 65) == 4
-    assert ops._pick_plan([], 128) == 4 and ops._pick_plan([], 129) == 5 and ops._pick_plan([], 8192) == 5
-    for M, bm in ((17, 64), (32, 64), (33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
+    assert ops._pick_plan([], 17) == 3 and ops._pick_plan([], 32) == 3 and ops._pick_plan([], 33) == 4
+    assert ops._pick_plan([], 64) == 4 and ops._pick_plan([], 65) == 5 and ops._pick_plan([], 128) == 5
+    assert ops._pick_plan([], 129) == 6 and ops._pick_plan([], 8192) == 6
+    for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
         assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm

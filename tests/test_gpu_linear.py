@@ -302,13 +302,15 @@ def test_baseline_config1_q8_0(dev):
 
 
 @pytest.mark.parametrize("n,K,M", [(1000, 2048, 300), (1000, 2048, 2148), (16384, 512, 1100),
-                                   (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120)],
+                                   (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120),
+                                   (1000, 2048, 20), (5120, 5120, 32), (200000, 256, 30)],
                          ids=str)
 def test_gemm_stream_k_schedule(dev, n, K, M):
-    """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows, 128 x 128 and 64 x 128
-    at 65..128 and 33..64): whole tiles dealt to the workgroups, the remainder tiles' k-steps split
-    over all of them (stream-K) and combined in k order by the last contributor.  Small grids are
-    all remainder; the 16384-row case at M=1100 and the 70000-row cases mix both phases.  Checked
+    """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows; 128 x 128, 64 x 128 and
+    32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
+    tiles' k-steps split over up to all of them (stream-K, >= 16 steps each, <= 6 per tile) and
+    combined in k order by the last contributor.  Small grids are all remainder; the 16384-row
+    case at M=1100 and the 70000- and 200000-row cases mix both phases.  Checked
     against an fp32 matmul of the GPU-dequantized weights (pinned bit-exact by the dequant
     tests), repeated launches bit-identical, counters back at zero."""
     import gguf_hip
@@ -325,4 +327,5 @@ def test_gemm_stream_k_schedule(dev, n, K, M):
     for _ in range(3):
         assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y)
     torch.cuda.synchronize()
-    assert int(gl.workspace[:256].abs().sum()) == 0            # the arrival counters
+    info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[:gguf_hip.ops._NPLAN])
+    assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0    # the arrival counters
