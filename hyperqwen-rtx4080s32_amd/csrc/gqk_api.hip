@@ -175,7 +175,14 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   const int64_t ctr_bytes = std::max(gqk_counter_bytes(tiles), gqk_counter_bytes(GQK_GEMM_MAX_WGS));
   if (ctr_bytes >= ((int64_t)1 << 31)) return fail(GQK_ERR_SHAPE, "plan: %lld tiles", (long long)tiles);
   pi.ctr_bytes = (int32_t)ctr_bytes;
-  if (M <= GQK_GEMV_MAX_M) {
+  // The GEMV serves up to 16 rows; layers with a table type (IQ4_NL / IQ4_XS / IQ3_S, whose
+  // lookups cost the GEMV the most per weight) switch to the 32-row GEMM above 8 rows, which
+  // measured faster there (IQ4_XS 34816 x 5120 at M = 16: 64 us GEMV, ~50 us GEMM).
+  bool table_type = false;
+  for (int i = 0; i < nshards; ++i)
+    table_type |= shards[i].ggml_type == GQK_IQ4_NL || shards[i].ggml_type == GQK_IQ4_XS || shards[i].ggml_type == GQK_IQ3_S;
+  const int gemv_max = table_type ? 8 : GQK_GEMV_MAX_M;
+  if (M <= gemv_max) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
 #ifdef GQK_GEMV_MIN_G
@@ -279,7 +286,6 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     return check_launch("linear (GEMV)");
   }
   if (info->form == GQK_FORM_GEMM) {
-    if (M <= GQK_GEMV_MAX_M) return fail(GQK_ERR_FORM, "linear: M=%d is served by the GEMV plan", M);
     if ((int64_t)M * ldx >= ((int64_t)1 << 40)) return fail(GQK_ERR_SHAPE, "linear: x too large");
     int rc = gqk::launch_gemm((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, K, y, ldy,
                               bias, info->bm, info->ctr_bytes, workspace, workspace_bytes, (hipStream_t)stream);

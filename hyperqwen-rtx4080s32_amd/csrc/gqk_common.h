@@ -125,7 +125,7 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 #define GQK_SPLIT_MAX 16   // split-K factor bound: the last workgroup loads every partial at once
 #define GQK_GEMM_MAX_WGS 1024   // persistent GEMM workgroups (up to three per CU) a launch may use: the counter region
 #ifndef GQK_GEMV_MAX_M
-#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form; the GEMM above
+#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form (8 for layers with an IQ type); the GEMM above
 #endif
 #define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
 enum {

@@ -28,8 +28,8 @@ extern "C" {
 #define GQK_ERR_HIP (-4)   /* HIP runtime error at launch */
 #define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
 
-#define GQK_FORM_GEMV 1 /* M <= 16: in-register decode GEMV (MFMA 4x4x4 per scale group) */
-#define GQK_FORM_GEMM 2 /* M > 16: LDS-dequant bf16 MFMA GEMM */
+#define GQK_FORM_GEMV 1 /* M <= 16 (<= 8 with an IQ shard): in-register decode GEMV (MFMA 4x4x4 per scale group) */
+#define GQK_FORM_GEMM 2 /* above: LDS-dequant bf16 MFMA GEMM (any M) */
 
 #define GQK_DTYPE_F32 0
 #define GQK_DTYPE_BF16 1
@@ -113,7 +113,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
  * that is 0) holding arrival counters (its first info->ctr_bytes bytes) and fp32 partials (after
  * them); it must be zero-filled before its first use, every launch leaves the counters at zero
  * again, one workspace serves every plan of one layer (any M: the counter region is the same in
- * all of them), and launches sharing one workspace must not overlap in time.  M must be <= info->m_max (and > 16 for a GEMM plan).  Replaces the grouped op
+ * all of them), and launches sharing one workspace must not overlap in time.  M must be <= info->m_max.  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
