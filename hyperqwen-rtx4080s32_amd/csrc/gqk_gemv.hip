@@ -65,17 +65,25 @@ __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int b) { return (
 // v_and_or_b32.  The values are hidden from constant folding by empty asm statements (no
 // instruction is emitted), so the compiler still schedules the ALU ops and their MFMA hazards.
 struct Masks {
-  uint32_t f, ff, t3, mg;   // 0x000F000F, 0x00FF00FF, 0x00030003 (SGPRs); 0x43004300 (VGPR)
+  uint32_t f, ff, t3, mg, m43;   // 0x000F000F, 0x00FF00FF, 0x00030003 (SGPRs); 0x43004300, 0x43434343 (VGPRs)
 };
 __device__ __forceinline__ Masks make_masks() {
-  Masks k{0x000F000Fu, 0x00FF00FFu, 0x00030003u, 0x43004300u};
+  Masks k{0x000F000Fu, 0x00FF00FFu, 0x00030003u, 0x43004300u, 0x43434343u};
   asm volatile("" : "+s"(k.f));
   asm volatile("" : "+s"(k.ff));
   asm volatile("" : "+s"(k.t3));
   asm volatile("" : "+v"(k.mg));
+  asm volatile("" : "+v"(k.m43));
   return k;
 }
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
+// Four byte values u0..u3 < 128 -> the two B dwords {128 + u0, 128 + u2} and {128 + u1, 128 + u3}
+// as bf16 pairs (the FAM_SWAP order): one v_perm_b32 each, placing a 0x43 exponent byte above
+// every value byte (v_perm selector bytes 0-3 pick bytes of the second source, 4-7 of the first).
+__device__ __forceinline__ void split_bytes(uint32_t u, const Masks& k, uint32_t& b0, uint32_t& b1) {
+  b0 = __builtin_amdgcn_perm(k.m43, u, 0x04020400u);
+  b1 = __builtin_amdgcn_perm(k.m43, u, 0x04030401u);
+}
 
 // Row r's slice of a plane of N bytes per row (N a multiple of 16).  Planes are column-major in
 // 16-byte columns: column i of row r sits at (i * 64 + r) * 16, so load i of a wave is one
@@ -120,8 +128,7 @@ template <> struct Dec<GQK_Q5_0> {
     uint32_t h4 = (qh[s] >> (4 * m)) & 0xFu;
     uint32_t hb = ((h4 * 0x00204081u) & 0x01010101u) << 4;   // bit i of h4 -> bit 4 of byte i
     uint32_t u = (w & 0x0F0F0F0Fu) | hb;
-    b0 = and_or(u, k.ff, k.mg);
-    b1 = and_or(u >> 8, k.ff, k.mg);
+    split_bytes(u, k, b0, b1);
   }
 };
 
@@ -178,8 +185,7 @@ template <> struct Dec<GQK_Q3_K> {
     uint32_t q = (qs[8 * n + 4 * hf + m] >> (2 * j)) & 0x03030303u;
     uint32_t h = (hm[4 * hf + m] >> (4 * n + j)) & 0x01010101u;
     uint32_t u = q | (h << 2);
-    b0 = and_or(u, k.ff, k.mg);
-    b1 = and_or(u >> 8, k.ff, k.mg);
+    split_bytes(u, k, b0, b1);
   }
 };
 
@@ -225,8 +231,7 @@ template <> struct Dec<GQK_Q5_K> {
   __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     uint32_t w = (qs[8 * (s >> 1) + m] >> (4 * (s & 1))) & 0x0F0F0F0Fu;
     uint32_t u = w | (((qh[m] >> s) & 0x01010101u) << 4);
-    b0 = and_or(u, k.ff, k.mg);
-    b1 = and_or(u >> 8, k.ff, k.mg);
+    split_bytes(u, k, b0, b1);
   }
 };
 
@@ -244,10 +249,11 @@ template <> struct Dec<GQK_Q6_K> {
   __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int h = s >> 3, t = (s >> 1) & 3, hf = s & 1;
     uint32_t lo = (ql[16 * h + 8 * (t & 1) + 4 * hf + m] >> (4 * (t >> 1))) & 0x0F0F0F0Fu;
-    uint32_t hi = (qh[8 * h + 4 * hf + m] >> (2 * t)) & 0x03030303u;
-    uint32_t u = lo | (hi << 4);
-    b0 = and_or(u, k.ff, k.mg);
-    b1 = and_or(u >> 8, k.ff, k.mg);
+    // the 2-bit high parts sit at bits 2t..2t+1 of each byte: moved to bits 4-5 and merged in one and_or
+    const uint32_t hr = qh[8 * h + 4 * hf + m];
+    const uint32_t hs = t == 0 ? hr << 4 : t == 1 ? hr << 2 : t == 2 ? hr : hr >> 2;
+    uint32_t u = and_or(hs, 0x30303030u, lo);
+    split_bytes(u, k, b0, b1);
   }
 };
 
