@@ -151,7 +151,8 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   pi.nb = (int32_t)nb;
   pi.n_total = n_total;
   std::vector<int32_t> rows;
-  auto row = [&](int i, int64_t tile0, int ntiles, int64_t kb0, int64_t kb1, int split, int64_t col0, int64_t ctr) {
+  auto row = [&](int i, int64_t tile0, int ntiles, int64_t kb0, int64_t kb1, int split, int64_t col0, int64_t ctr,
+                 int nc = 1, int64_t slot0 = 0) {
     int32_t r[GQK_DESC_WORDS] = {0};
     r[D_TYPE] = shards[i].ggml_type;
     r[D_OFF_LO] = (int32_t)(uint32_t)(shards[i].offset & 0xFFFFFFFF);
@@ -165,6 +166,8 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     r[D_NVALID] = (int32_t)std::min<int64_t>((int64_t)ntiles * 64, shards[i].n - tile0 * 64);
     r[D_NB] = (int32_t)nb;
     r[D_CTR] = (int32_t)ctr;
+    r[D_NC] = nc;
+    r[D_SLOT0] = (int32_t)slot0;
     rows.insert(rows.end(), r, r + GQK_DESC_WORDS);
   };
   int64_t tiles = 0;
@@ -200,19 +203,40 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
     const int64_t split =
         std::max<int64_t>(1, std::min({(per_tile + nw - 1) / nw, nb / nw, (int64_t)GQK_SPLIT_MAX}));
+    // Tail: with whole tiles (split 1) in more than one round of resident workgroups (target / nw
+    // of them, two per CU at the default target), a last round of r <= half the slots would put
+    // a third whole tile on r CUs, which then finish last (gate_up's 544 tiles on 256 CUs: 28.5 us
+    // against 22.2 us for 512).  Those r tiles split K instead, into workgroups of >= one record a
+    // wave, so their work spreads over up to half the CUs as light extra workgroups.
+    const int64_t slots = std::max<int64_t>(1, target / nw);
+    int64_t tail = 0, split_tail = 1;
+    if (split == 1 && tiles > slots) {
+      const int64_t r = tiles % slots;
+      if (r > 0 && 2 * r <= slots) split_tail = std::min<int64_t>({nb / nw, std::max<int64_t>(1, slots / 2 / r),
+                                                                   (int64_t)GQK_SPLIT_MAX});
+      if (split_tail > 1) tail = r;
+    }
     pi.nw = (int32_t)nw;
-    pi.split = (int32_t)split;
-    int64_t col0 = 0, ctr = 0;
+    pi.split = (int32_t)std::max(split, split_tail);
+    int64_t col0 = 0, g = 0, ctr = 0, slot = 0;
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
-      for (int64_t t0 = 0; t0 < ntile; ++t0, ++ctr)
-        for (int64_t s = 0; s < split; ++s)   // balanced partition: every split owns >= 1 super-block
-          row(i, t0, 1, s * nb / split, (s + 1) * nb / split, (int)s, col0, ctr);
+      for (int64_t t0 = 0; t0 < ntile; ++t0, ++g) {
+        const int64_t sp = g >= tiles - tail ? split_tail : split;
+        if (sp == 1) {
+          row(i, t0, 1, 0, nb, 0, col0, 0);
+          continue;
+        }
+        for (int64_t s = 0; s < sp; ++s)   // balanced partition: every split owns >= 1 super-block
+          row(i, t0, 1, s * nb / sp, (s + 1) * nb / sp, (int)s, col0, ctr, (int)sp, slot);
+        ++ctr;
+        slot += sp;
+      }
       col0 += shards[i].n;
     }
-    // workspace: the counter region (one arrival counter per tile; zero before the first launch,
-    // left zero by each launch), then the fp32 partials [tile][split][64 rows][m_max tokens]
-    pi.workspace_bytes = split > 1 ? ctr_bytes + gqk_partial_bytes(tiles, split, pi.m_max) : 0;
+    // workspace: the counter region (one arrival counter per split tile; zero before the first
+    // launch, left zero by each launch), then the fp32 partial slots [slot][64 rows][m_max tokens]
+    pi.workspace_bytes = slot > 0 ? ctr_bytes + gqk_partial_bytes(slot, 1, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
     // 32 / 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens
@@ -243,7 +267,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
 int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
   if (!info) return fail(GQK_ERR_ARG, "linear_workspace_bytes: info is NULL");
   if (M <= 0) return 0;
-  if (info->form == GQK_FORM_GEMV) return info->split > 1 ? info->workspace_bytes : 0;
+  if (info->form == GQK_FORM_GEMV) return info->workspace_bytes;
   if (info->form == GQK_FORM_GEMM) {
     const int64_t n = gqk::gemm_workspace(info->bm, info->n_desc, M, info->nb, info->ctr_bytes);
     return n < 0 ? fail(GQK_ERR_HIP, "linear_workspace_bytes: no HIP device") : n;
@@ -266,14 +290,13 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
   if (info->form == GQK_FORM_GEMV) {
     if (M > info->m_max) return fail(GQK_ERR_FORM, "linear: M=%d above the GEMV plan's %d rows", M, info->m_max);
     if (info->g != 1 && info->g != 2 && info->g != 4 && info->g != 8) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
-    int64_t tiles = 0;
     int* counters = nullptr;
     float* partials = nullptr;
-    if (info->split > 1) {
-      tiles = info->n_desc / info->split;   // one descriptor row per (tile, split)
-      const int64_t cb = info->ctr_bytes;
-      if (cb < gqk_counter_bytes(tiles)) return fail(GQK_ERR_FORM, "linear: counter region %lld bytes", (long long)cb);
-      const int64_t need = cb + gqk_partial_bytes(tiles, info->split, 4 * info->g);
+    if (info->workspace_bytes > 0) {
+      // counters at the start (one per split tile, fewer than the descriptor rows), partial slots after
+      const int64_t cb = info->ctr_bytes, need = info->workspace_bytes;
+      if (cb <= 0 || (cb & 255) || need <= cb)
+        return fail(GQK_ERR_FORM, "linear: counter region %lld / workspace %lld bytes", (long long)cb, (long long)need);
       if (!workspace || workspace_bytes < need)
         return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);
       if ((uintptr_t)workspace & 255) return fail(GQK_ERR_SHAPE, "linear: workspace not 256-byte aligned");
@@ -281,7 +304,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
       partials = (float*)((char*)workspace + cb);
     }
     int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw, y,
-                              ldy, bias, partials, counters, info->split, (hipStream_t)stream);
+                              ldy, bias, partials, counters, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }

@@ -141,6 +141,8 @@ enum {
   D_NVALID = 9,   // valid output rows from D_COL0 (the shard's last tile is partial)
   D_NB = 10,      // super-blocks per row (K / 256)
   D_CTR = 11,     // GEMV split-K: arrival counter of the row's tile (index into the counters)
+  D_NC = 12,      // GEMV: workgroups (rows) sharing the row's tile; 1 = the row writes y itself
+  D_SLOT0 = 13,   // GEMV split-K: first fp32 partial slot of the row's tile (slot D_SLOT0 + D_SPLIT)
 };
 
 #ifdef __cplusplus

@@ -23,8 +23,8 @@
 // bf16 x exact-integer are exact in the MFMA, accumulation is fp32, so the result equals an
 // fp32 matmul of the gguf-py weights up to summation order.
 //
-// Split-K: with more than one k-range per tile the workgroups write fp32 partials
-// [tile][split][row][token]; the last workgroup of a tile to arrive sums them in split order
+// Split-K: a tile shared by several workgroups (k-ranges) gets fp32 partial slots
+// [slot][row][token]; the last workgroup of the tile to arrive sums them in split order
 // (deterministic, one rounding to bf16), the reference's sum_partials
 // (gguf-plugin/gluon/tiles_grouped.py:142-162) fused into the same launch.
 #include <hip/hip_runtime.h>
@@ -516,9 +516,9 @@ __host__ __device__ constexpr int gemv_lds_bytes(int nw, bool tables) {
 
 // One workgroup of nw waves (blockDim.x / 64, at most GQK_GEMV_MAX_WAVES) per descriptor row: one
 // 64-row tile, its k-range split evenly over the waves, the waves' sums combined through LDS in
-// a fixed order; with split-K (part != nullptr) the fp32 partial goes to the tile's partial slot
-// and the last workgroup of the tile to arrive (counter ctr[tile]) sums the partials in split
-// order and writes y, then resets the counter.
+// a fixed order.  A tile covered by one row (D_NC = 1) is written to y; a tile shared by D_NC rows
+// (split-K) sends its fp32 partial to slot D_SLOT0 + D_SPLIT, and the last workgroup of the tile
+// to arrive (counter ctr[D_CTR]) sums the partials in split order, writes y and resets the counter.
 // Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 fits
 // three waves without spilling and runs faster there than at the allocator's own choice of two.
 template <int G, int ONLY>
@@ -534,7 +534,7 @@ template <int G, int ONLY>
 __global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>())))
 void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
                  int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ bias,
-                 float* __restrict__ part, int* __restrict__ ctr, int split) {
+                 float* __restrict__ part, int* __restrict__ ctr) {
   constexpr int MPAD = 4 * G;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
@@ -580,7 +580,8 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   const int64_t col = (int64_t)dsc[D_COL0] + lane;
   // the layer bias (bf16 per output column) joins before the one rounding to bf16
   const float bv = bias != nullptr && row_ok ? __builtin_bit_cast(float, (uint32_t)bias[col] << 16) : 0.f;
-  if (part == nullptr) {
+  const int nc = dsc[D_NC];   // workgroups sharing this tile
+  if (nc == 1) {
     if (row_ok)
 #pragma unroll
       for (int g = 0; g < G; ++g)
@@ -591,13 +592,15 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
         }
     return;
   }
-  // Split-K exchange.  The partials of a tile sit at part[tile][split][lane][MPAD] (1 KiB x G per
-  // workgroup, written as 16-byte stores).  They move through device-coherent (sc1) buffer
-  // accesses only, which write through / bypass the per-XCD L2's non-coherent lines, and the
-  // stores complete before the arrival count: no L2-wide writeback or invalidate is needed.
+  // Split-K exchange.  The nc partials of a tile sit in its slots D_SLOT0 .. D_SLOT0 + nc - 1 as
+  // [slot][lane][MPAD] (1 KiB x G per workgroup, written as 16-byte stores).  They move through
+  // device-coherent (sc1) buffer accesses only, which write through / bypass the per-XCD L2's
+  // non-coherent lines, and the stores complete before the arrival count: no L2-wide writeback
+  // or invalidate is needed.
   const int s = dsc[D_SPLIT];
   const int ctr_i = dsc[D_CTR];
-  float* tp = part + (int64_t)ctr_i * split * 64 * MPAD;
+  const int split = nc;
+  float* tp = part + (int64_t)dsc[D_SLOT0] * 64 * MPAD;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, split * 64 * MPAD * 4, GQK_BUF_WORD3);
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -641,34 +644,34 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
 template <int G>
 static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
                      const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, const uint16_t* bias,
-                     float* part, int* ctr, int split) {
+                     float* part, int* ctr) {
   const bool iq = only == 0 || only == GQK_IQ4_NL || only == GQK_IQ4_XS || only == GQK_IQ3_S;
   const size_t lds = (size_t)gemv_lds_bytes<G>(nw, iq);
   const dim3 block(64 * nw);
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr, split); return;
+#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr); return;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr, split);
+      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr);
   }
 }
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, int nw, void* y, int64_t ldy, const void* bias, float* partials, int* counters, int split,
+                int M, int G, int nw, void* y, int64_t ldy, const void* bias, float* partials, int* counters,
                 hipStream_t st) {
   if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
   dim3 grid(n_desc);
-  float* part = split > 1 ? partials : nullptr;
+  float* part = partials;
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
   switch (G) {
-    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
-    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
-    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters, split); break;
+    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
+    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
+    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
     default: return GQK_ERR_FORM;
   }
   return GQK_OK;

@@ -71,31 +71,88 @@ def _rows(desc):
     return desc.numpy().reshape(-1, 16)
 
 
+def _check_gemv_rows(shards, K, info, desc):
+    """The GEMV plan's per-row contract: every 64-row tile covered by nc rows (D_NC) whose k-ranges
+    split [0, nb) evenly in split order (D_SPLIT = 0..nc-1); a split tile (nc > 1) has its own
+    arrival counter and nc consecutive partial slots from D_SLOT0; the workspace holds the counter
+    region and every slot.  Returns {tile: nc}."""
+    nb = K // 256
+    d = _rows(desc)
+    assert info.form == 1 and d.shape[0] == info.n_desc
+    by_tile = {}
+    for row in d:
+        assert row[4] == 1 and row[10] == nb
+        by_tile.setdefault((int(row[1]) | int(row[2]) << 32, int(row[3])), []).append(row)
+    assert len(by_tile) == sum((n + 63) // 64 for _, n, _ in shards)
+    ctrs, slots, ncs = [], [], {}
+    for key, rows in by_tile.items():
+        nc = len(rows)
+        ncs[key] = nc
+        assert [int(r[12]) for r in rows] == [nc] * nc and [int(r[7]) for r in rows] == list(range(nc))
+        assert [(int(r[5]), int(r[6])) for r in rows] == [(j * nb // nc, (j + 1) * nb // nc) for j in range(nc)]
+        if nc > 1:
+            assert len({int(r[11]) for r in rows}) == 1 and len({int(r[13]) for r in rows}) == 1
+            ctrs.append(int(rows[0][11]))
+            slots.append((int(rows[0][13]), nc))
+    assert sorted(ctrs) == list(range(len(ctrs)))
+    slots.sort()
+    assert all(a + n == b for (a, n), (b, _) in zip(slots, slots[1:])) and (not slots or slots[0][0] == 0)
+    n_slots = sum(n for _, n in slots)
+    assert info.workspace_bytes == (info.ctr_bytes + n_slots * 64 * info.m_max * 4 if n_slots else 0)
+    assert info.split == max(ncs.values())
+    return ncs
+
+
 def test_plan_gemv_balanced_split_partition():
     from gguf_hip import ops
 
     for target in (1, 16, 97, 1024, 4096, 0):
         info, desc = ops.plan([(21, 6144, 0)], 20 * 256, 1, target)
-        d = _rows(desc)
+        ncs = _check_gemv_rows([(21, 6144, 0)], 20 * 256, info, desc)
         S, nw = info.split, info.nw
         assert info.form == 1 and info.g == 1 and info.m_max == 4
         assert 1 <= nw <= 4 and S * nw <= 20                # every wave keeps >= 1 super-block
         if S > 1:
             assert nw == 4                                  # K splits across workgroups only past a full one
-        assert d.shape[0] == info.n_desc == 96 * S          # one workgroup per (64-row tile, split)
-        first = d[d[:, 3] == 0]                             # the workgroups of tile 0
-        assert first[:, 5].tolist() == [s * 20 // S for s in range(S)]
-        assert first[:, 6].tolist() == [(s + 1) * 20 // S for s in range(S)]
-        assert first[:, 7].tolist() == list(range(S)) and (first[:, 11] == 0).all()
-        assert sorted(set(d[:, 11].tolist())) == list(range(96))   # one arrival counter per tile
+        assert set(ncs.values()) == {S}                     # 96 tiles: one round or whole rounds, no tail
         # the counter region: one int per tile, at least the GEMM's 1024 workgroups, 256-byte rounded
         assert info.ctr_bytes == 4096
-        assert info.workspace_bytes == (4096 + S * 4 * 6144 * 4 if S > 1 else 0)
     assert ops.plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
     info = ops.plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
     assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
     info = ops.plan([(21, 6144, 0)], 20 * 256, 8, 0)[0]
     assert (info.nw, info.split) == (4, 5)                  # default target 2048 waves: 22 per tile
+
+
+def test_plan_gemv_tail_tiles_split():
+    """Whole tiles beyond full rounds of resident workgroups: a short last round (<= half the
+    slots) splits K instead of putting a third whole tile on a few CUs."""
+    from gguf_hip import ops
+
+    # gate_up 34816 x 5120 at the default target: 544 tiles, 512 slots of 4 waves -> 512 whole
+    # tiles, the last 32 split 5 ways (>= one record per wave; up to 8 would fit half the slots)
+    info, desc = ops.plan([(12, 34816, 0)], 5120, 8, 0)
+    ncs = _check_gemv_rows([(12, 34816, 0)], 5120, info, desc)
+    order = [ncs[k] for k in sorted(ncs, key=lambda k: k[1])]
+    assert order == [1] * 512 + [5] * 32 and info.n_desc == 512 + 160 and info.nw == 4
+    # a full last round (no remainder) and a long one (> half the slots) stay whole
+    info, desc = ops.plan([(12, 32768, 0)], 5120, 8, 0)
+    assert set(_check_gemv_rows([(12, 32768, 0)], 5120, info, desc).values()) == {1} and info.workspace_bytes == 0
+    info, desc = ops.plan([(12, 64 * 13, 0)], 16 * 256, 1, 16)     # 13 tiles, 8 slots of 2 waves
+    assert info.nw == 2 and set(_check_gemv_rows([(12, 64 * 13, 0)], 16 * 256, info, desc).values()) == {1}
+    # 800 tiles at the default target: 3 waves each, 682 slots, the last 118 tiles split 2 ways
+    info, desc = ops.plan([(12, 64 * 800, 0)], 5120, 8, 0)
+    ncs = _check_gemv_rows([(12, 64 * 800, 0)], 5120, info, desc)
+    assert info.nw == 3 and sorted(ncs.values()) == [1] * 682 + [2] * 118
+    # the tail spans shards: Q6_K 34816 rows after a 1024-row Q4_K shard (560 tiles, 48 split)
+    off = ops.tiles_bytes(12, 1024, 5120)
+    info, desc = ops.plan([(12, 1024, 0), (14, 34816, off)], 5120, 1, 0)
+    ncs = _check_gemv_rows([(12, 1024, 0), (14, 34816, off)], 5120, info, desc)
+    assert sum(1 for v in ncs.values() if v > 1) == 48 and info.split == min(5, 256 // 48)
+    # small targets: 10 tiles on 8 slots of 2 waves... (target 16) -> the last 2 tiles split
+    info, desc = ops.plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
+    ncs = _check_gemv_rows([(12, 64 * 9 + 17, 0)], 16 * 256, info, desc)
+    assert info.nw == 2 and sorted(ncs.values()) == [1] * 8 + [2, 2]
 
 
 def test_plan_descriptor_rows_mixed_layer():
@@ -115,7 +172,8 @@ def test_plan_descriptor_rows_mixed_layer():
     assert d[:, 0].tolist() == [21, 21, 12, 12, 12, 12, 12]
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
     assert d[:, 8].tolist() == [0, 64, 70, 134, 198, 262, 326] and d[:, 9].tolist() == [64, 6, 64, 64, 64, 64, 44]
-    assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 11].tolist() == list(range(7))
+    assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 12].tolist() == [1] * 7   # whole tiles
+    _check_gemv_rows([(21, 70, 0), (12, 300, off2)], K, info, desc)
     assert info.nw == 1                                     # a target of 4 waves for 7 tiles: one each
     gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 100)
     g = _rows(gd)

@@ -88,6 +88,31 @@ def test_split_k_repeat_is_bit_identical(dev):
     assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
 
 
+@pytest.mark.parametrize("wt", [G.Q4_K, G.Q6_K, G.IQ3_S, G.Q8_0], ids=lambda t: G.NAMES[t])
+def test_gemv_tail_tiles_split(dev, wt):
+    """A plan with whole tiles and a split tail (10 tiles on 8 resident slots at target 16: the
+    last two tiles split K over two workgroups each, the rest written directly): matches the
+    oracle, repeats bit-identically, and leaves the counters at zero."""
+    import gguf_hip
+
+    rng = np.random.default_rng(40 + wt)
+    n, K = 64 * 9 + 17, 16 * 256
+    raw = G.random_blocks(rng, n, K, wt)
+    wf = G.dequantize(raw, wt)
+    gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt], target_wgs=16)
+    for M in (1, 5, 8):
+        i = gguf_hip.ops._pick_plan(gl.plans, M)
+        info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[i * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
+        assert info.form == 1 and info.split == 2 and info.n_desc == 8 + 2 * 2
+        x = _x(M, K, 4100 + M, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
+        for _ in range(5):
+            assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y)
+    torch.cuda.synchronize()
+    assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
+
+
 def test_one_workspace_serves_every_form(dev):
     """One layer workspace across the GEMV (split tiles) and the three GEMM forms (stream-K
     partials) in an order where each form's partials would land on another form's counters if
