@@ -218,11 +218,23 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     }
     pi.nw = (int32_t)nw;
     pi.split = (int32_t)std::max(split, split_tail);
+    // One round of split tiles whose waves stream >= 2 records each: fill the resident slots
+    // exactly (s0 or s0 + 1 rows per tile) rather than overshoot them and leave a few CUs a third
+    // workgroup (down 5120 x 17408: 560 -> 512 workgroups, Q6_K M = 1 26.0 -> 21.3 us).  With one
+    // record per wave (qkv, o_proj at K = 5120) the extra workgroups' memory parallelism wins.
+    int64_t s0 = split, extra = 0;
+    if (split > 1 && tiles <= slots && nb >= 2 * split * nw) {
+      const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(nb / nw, GQK_SPLIT_MAX));
+      const int64_t total = std::min(slots, tiles * smax);
+      s0 = std::max<int64_t>(1, total / tiles);
+      extra = s0 < smax ? total - s0 * tiles : 0;
+      pi.split = (int32_t)(s0 + (extra > 0));
+    }
     int64_t col0 = 0, g = 0, ctr = 0, slot = 0;
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
       for (int64_t t0 = 0; t0 < ntile; ++t0, ++g) {
-        const int64_t sp = g >= tiles - tail ? split_tail : split;
+        const int64_t sp = g >= tiles - tail ? split_tail : split > 1 ? s0 + (g < extra) : split;
         if (sp == 1) {
           row(i, t0, 1, 0, nb, 0, col0, 0);
           continue;

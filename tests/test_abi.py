@@ -149,6 +149,13 @@ def test_plan_gemv_tail_tiles_split():
     info, desc = ops.plan([(12, 1024, 0), (14, 34816, off)], 5120, 1, 0)
     ncs = _check_gemv_rows([(12, 1024, 0), (14, 34816, off)], 5120, info, desc)
     assert sum(1 for v in ncs.values() if v > 1) == 48 and info.split == min(5, 256 // 48)
+    # one round of split tiles with >= 2 records a wave fills the 512 slots exactly: down 5120 x
+    # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; qkv (1 record a wave) keeps 5 each
+    info, desc = ops.plan([(12, 5120, 0)], 17408, 8, 0)
+    ncs = _check_gemv_rows([(12, 5120, 0)], 17408, info, desc)
+    assert info.n_desc == 512 and sorted(ncs.values()) == [6] * 48 + [7] * 32 and info.split == 7
+    info, desc = ops.plan([(12, 7168, 0)], 5120, 8, 0)
+    assert set(_check_gemv_rows([(12, 7168, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 560
     # small targets: 10 tiles on 8 slots of 2 waves... (target 16) -> the last 2 tiles split
     info, desc = ops.plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
     ncs = _check_gemv_rows([(12, 64 * 9 + 17, 0)], 16 * 256, info, desc)
