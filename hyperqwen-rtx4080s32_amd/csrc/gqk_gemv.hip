@@ -452,6 +452,17 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
   // decode) covers exactly the loads it needs under the in-order vmcnt count.  Every load is
   // unconditional (addresses clamped to the wave's last super-block, so the tail re-reads it
   // from L2) and the buffers rotate by code position, never by copy.
+  if (G <= 2 && kw1 - kw0 == 1) {
+    // a single record: no pipeline, so no clamped follow-up loads for the workgroup barrier's
+    // vmcnt(0) to wait on (the waves of the K = 5120 shards split 5 ways hold one record each)
+    uint4 xs[NI][4];
+    D r;
+    stage_load<MPAD>(x, ldx, M, kw0, lane, xs);
+    r.load(tbase + (int64_t)kw0 * (64 * D::REC), lane);
+    stage_store<MPAD, D::FAM>(wl, M, lane, xs);
+    process(r);
+    return;
+  }
   constexpr int DEPTH = gemv_depth<G, T>();
   const int last = kw1 - 1;
   auto rec = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
