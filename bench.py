@@ -133,8 +133,8 @@ def cpu_baseline(seconds: float = 15.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=8, help="batch rows of the decode GEMV (1..32)")
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 1 GB in total)")
     ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
