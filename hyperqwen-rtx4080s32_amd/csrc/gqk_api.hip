@@ -231,21 +231,28 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
       pi.split = (int32_t)(s0 + (extra > 0));
     }
     int64_t col0 = 0, g = 0, ctr = 0, slot = 0;
+    bool one_record = true;   // every wave of every row streams exactly one record
     for (int i = 0; i < nshards; ++i) {
       int64_t ntile = (shards[i].n + 63) / 64;
       for (int64_t t0 = 0; t0 < ntile; ++t0, ++g) {
         const int64_t sp = g >= tiles - tail ? split_tail : split > 1 ? s0 + (g < extra) : split;
         if (sp == 1) {
           row(i, t0, 1, 0, nb, 0, col0, 0);
+          one_record &= nb == nw;
           continue;
         }
-        for (int64_t s = 0; s < sp; ++s)   // balanced partition: every split owns >= 1 super-block
+        for (int64_t s = 0; s < sp; ++s) {   // balanced partition: every split owns >= 1 super-block
           row(i, t0, 1, s * nb / sp, (s + 1) * nb / sp, (int)s, col0, ctr, (int)sp, slot);
+          one_record &= (s + 1) * nb / sp - s * nb / sp == nw;
+        }
         ++ctr;
         slot += sp;
       }
       col0 += shards[i].n;
     }
+    // a plan whose waves all hold a single record launches the kernel built without the register
+    // pipeline (fewer registers: more workgroups resident), flagged in the GEMM-only bm field
+    pi.bm = one_record ? 1 : 0;
     // workspace: the counter region (one arrival counter per split tile; zero before the first
     // launch, left zero by each launch), then the fp32 partial slots [slot][64 rows][m_max tokens]
     pi.workspace_bytes = slot > 0 ? ctr_bytes + gqk_partial_bytes(slot, 1, pi.m_max) : 0;
@@ -315,8 +322,8 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
       counters = (int*)workspace;
       partials = (float*)((char*)workspace + cb);
     }
-    int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw, y,
-                              ldy, bias, partials, counters, (hipStream_t)stream);
+    int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw,
+                              info->bm == 1, y, ldy, bias, partials, counters, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }

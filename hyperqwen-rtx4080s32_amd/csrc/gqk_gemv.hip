@@ -398,8 +398,14 @@ __host__ __device__ constexpr int gemv_depth() {
 #endif
 }
 
-// One wave: weight rows of tile `tile`, super-blocks [kw0, kw1), accumulating into acc.
-template <int G, int T>
+template <int G, int T, class P>
+__device__ __forceinline__ void gemv_pipeline(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
+                                              int64_t ldx, int M, int kw0, int kw1, uint8_t* wl, int lane,
+                                              const P& process);
+
+// One wave: weight rows of tile `tile`, super-blocks [kw0, kw1), accumulating into acc.  ONE: the
+// launch guarantees kw1 - kw0 == 1 for every wave (only the pipeline-free path is compiled).
+template <int G, int T, bool ONE>
 __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
                                           int64_t ldx, int M, int kw0, int kw1, uint8_t* wl, const Tabs& tb,
                                           const Masks& mk, v4f (&acc)[G]) {
@@ -446,13 +452,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
     }
   };
 
-  // Register pipeline DEPTH super-blocks deep: while record kb is decoded, the records (and the
-  // x slices) of kb+1 .. kb+DEPTH-1 are in flight.  Each step issues x(kb+DEPTH) and then the
-  // record kb+DEPTH, so every wait (x of a step before its LDS write, the record before its
-  // decode) covers exactly the loads it needs under the in-order vmcnt count.  Every load is
-  // unconditional (addresses clamped to the wave's last super-block, so the tail re-reads it
-  // from L2) and the buffers rotate by code position, never by copy.
-  if (G <= 2 && kw1 - kw0 == 1) {
+  if (ONE || (G <= 2 && kw1 - kw0 == 1)) {
     // a single record: no pipeline, so no clamped follow-up loads for the workgroup barrier's
     // vmcnt(0) to wait on (the waves of the K = 5120 shards split 5 ways hold one record each)
     uint4 xs[NI][4];
@@ -463,6 +463,21 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
     process(r);
     return;
   }
+  if constexpr (!ONE) gemv_pipeline<G, T>(tbase, x, ldx, M, kw0, kw1, wl, lane, process);
+}
+
+// The register pipeline of a wave with two or more records, DEPTH super-blocks deep: while
+// record kb is decoded, the records (and the x slices) of kb+1 .. kb+DEPTH-1 are in flight.  Each
+// step issues x(kb+DEPTH) and then the record kb+DEPTH, so every wait (x of a step before its LDS
+// write, the record before its decode) covers exactly the loads it needs under the in-order
+// vmcnt count.  Every load is unconditional (addresses clamped to the wave's last super-block, so
+// the tail re-reads it from L2) and the buffers rotate by code position, never by copy.
+template <int G, int T, class P>
+__device__ __forceinline__ void gemv_pipeline(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
+                                              int64_t ldx, int M, int kw0, int kw1, uint8_t* wl, int lane,
+                                              const P& process) {
+  typedef Dec<T> D;
+  constexpr int MPAD = 4 * G, NI = (8 * MPAD + 63) / 64;
   constexpr int DEPTH = gemv_depth<G, T>();
   const int last = kw1 - 1;
   auto rec = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
@@ -541,8 +556,8 @@ constexpr int gemv_waves() {
 #endif
 }
 
-template <int G, int ONLY>
-__global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(gemv_waves<G, ONLY>())))
+template <int G, int ONLY, bool ONE>
+__global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) __attribute__((amdgpu_waves_per_eu(ONE ? 1 : gemv_waves<G, ONLY>())))
 void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
                  int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ bias,
                  float* __restrict__ part, int* __restrict__ ctr) {
@@ -570,7 +585,7 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
 
 #define RUN(T)                                                                                           \
   if ((ONLY == 0 || ONLY == T) && type == T)                                                             \
-    gemv_wave<G, T>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, wl, tb, mk, acc);
+    gemv_wave<G, T, ONE>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, wl, tb, mk, acc);
   RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
   RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
@@ -652,7 +667,7 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
-template <int G>
+template <int G, bool ONE>
 static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
                      const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, const uint16_t* bias,
                      float* part, int* ctr) {
@@ -660,18 +675,18 @@ static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t*
   const size_t lds = (size_t)gemv_lds_bytes<G>(nw, iq);
   const dim3 block(64 * nw);
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr); return;
+#define C(T) case T: hipLaunchKernelGGL((gemv_kernel<G, T, ONE>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr); return;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C
     default:
-      hipLaunchKernelGGL((gemv_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr);
+      hipLaunchKernelGGL((gemv_kernel<G, 0, ONE>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias, part, ctr);
   }
 }
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, int nw, void* y, int64_t ldy, const void* bias, float* partials, int* counters,
+                int M, int G, int nw, bool one, void* y, int64_t ldy, const void* bias, float* partials, int* counters,
                 hipStream_t st) {
   if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
   dim3 grid(n_desc);
@@ -680,9 +695,13 @@ int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int type
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
   switch (G) {
-    case 1: launch_g<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
-    case 2: launch_g<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
-    case 4: launch_g<4>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); break;
+#define L(GG)                                                                                              \
+    if (one) launch_g<GG, true>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); \
+    else launch_g<GG, false>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters);
+    case 1: L(1) break;
+    case 2: L(2) break;
+    case 4: L(4) break;
+#undef L
     default: return GQK_ERR_FORM;
   }
   return GQK_OK;

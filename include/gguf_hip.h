@@ -48,7 +48,8 @@ typedef struct gqk_plan_info {
   int32_t form;       /* GQK_FORM_GEMV or GQK_FORM_GEMM */
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
   int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4) */
-  int32_t bm;         /* GEMM: tokens per tile (64, 128, 256) */
+  int32_t bm;         /* GEMM: tokens per tile (32, 64, 128, 256); GEMV: 1 when every wave streams
+                         exactly one 256-weight record (the launch takes the pipeline-free kernel) */
   int32_t split;      /* GEMV: most workgroups sharing one tile (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */

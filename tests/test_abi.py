@@ -156,6 +156,10 @@ def test_plan_gemv_tail_tiles_split():
     assert info.n_desc == 512 and sorted(ncs.values()) == [6] * 48 + [7] * 32 and info.split == 7
     info, desc = ops.plan([(12, 7168, 0)], 5120, 8, 0)
     assert set(_check_gemv_rows([(12, 7168, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 560
+    # the GEMV's bm field flags plans whose waves all stream exactly one record (qkv, o_proj at
+    # K = 5120: 20 records = 5 workgroups x 4 waves); the pipeline-free kernel serves them
+    assert info.bm == 1 and ops.plan([(12, 5120, 0)], 5120, 1, 0)[0].bm == 1
+    assert ops.plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0 and ops.plan([(12, 5120, 0)], 17408, 8, 0)[0].bm == 0
     # small targets: 10 tiles on 8 slots of 2 waves... (target 16) -> the last 2 tiles split
     info, desc = ops.plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
     ncs = _check_gemv_rows([(12, 64 * 9 + 17, 0)], 16 * 256, info, desc)
