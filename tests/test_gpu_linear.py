@@ -113,6 +113,67 @@ def test_gemv_tail_tiles_split(dev, wt):
     assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
 
 
+def test_graph_replay_matches_eager(dev):
+    """The grouped op captured in one HIP graph, as a serving loop (and bench.py) runs it: the
+    GEMV with split-K partials and in-kernel counters, the GEMV with a split tail, with a fused
+    bias, and the stream-K GEMM in its 32-row and 256-row forms.  Five replays, each after new x
+    is copied into the captured inputs, followed by eager launches of the same layers (sharing
+    the layers' workspaces) and a host synchronisation: every replay is bit-identical to the
+    eager result on the same x, which matches the oracle, and the counters end at zero (they are
+    reset by the kernels themselves, so the graph holds no memset)."""
+    import gguf_hip
+    from gguf_hip.synth import random_shard
+
+    cases = [  # (type, n, K, M, target_wgs, bias)
+        (G.Q4_K, 900, 12 * 256, 8, 0, False),        # GEMV, split K
+        (G.Q6_K, 900, 12 * 256, 1, 0, True),         # GEMV, split K, fused bf16 bias
+        (G.IQ4_XS, 64 * 9 + 17, 16 * 256, 5, 16, False),   # GEMV, whole tiles + split tail
+        (G.Q5_K, 1000, 2048, 20, 0, False),          # GEMM 32 x 128, stream-K only
+        (G.Q4_K, 1000, 2048, 300, 0, True),          # GEMM 256 x 256, stream-K, bias
+    ]
+    layers, xs, biases, wfs = [], [], [], []
+    for i, (wt, n, K, M, tw, has_bias) in enumerate(cases):
+        W = random_shard(n, K, wt, dev, seed=700 + i)
+        wfs.append(gguf_hip.dequantize(W, wt, (n, K), torch.float32))
+        layers.append(gguf_hip.pack_layer([W], [n], [wt], target_wgs=tw))
+        xs.append(_x(M, K, 7000 + i, dev))
+        biases.append(torch.randn(n, device=dev).to(torch.bfloat16) if has_bias else None)
+    for gl, (wt, n, K, M, tw, _) in zip(layers, cases):
+        info = gguf_hip.ops.GqkPlanInfo.from_tuple(
+            gl.plans[gguf_hip.ops._pick_plan(gl.plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
+        assert info.form == (1 if M <= 8 else 2) and (M > 8 or info.split > 1), (G.NAMES[wt], M)
+
+    def run():
+        return [gguf_hip.mul_mat_grouped(x, gl, b) for x, gl, b in zip(xs, layers, biases)]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):      # eager warm-up: workspaces and device tables exist before capture
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ys = run()
+    gen = torch.Generator(device=dev).manual_seed(99)
+    for rep in range(5):
+        for x in xs:
+            x.copy_(torch.randn(x.shape, device=dev, generator=gen).to(torch.bfloat16))
+        graph.replay()
+        eager = run()
+        torch.cuda.synchronize()
+        for i, (y, e) in enumerate(zip(ys, eager)):
+            assert torch.equal(y, e), (rep, i)
+        if rep == 0:
+            for y, x, wf, b in zip(ys, xs, wfs, biases):
+                ref = x.float() @ wf.T + (b.float() if b is not None else 0.0)
+                scale = ref.abs().amax(dim=1, keepdim=True).clamp(min=1e-30)
+                assert float(((y.float() - ref).abs() / scale).amax()) < TOL
+    for gl in layers:
+        info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[:gguf_hip.ops._NPLAN])
+        assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
+
+
 def test_one_workspace_serves_every_form(dev):
     """One layer workspace across the GEMV (split tiles) and the three GEMM forms (stream-K
     partials) in an order where each form's partials would land on another form's counters if
