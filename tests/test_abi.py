@@ -166,6 +166,63 @@ def test_plan_gemv_tail_tiles_split():
     assert info.nw == 2 and sorted(ncs.values()) == [1] * 8 + [2, 2]
 
 
+def test_plan_random_layers_stay_in_bounds():
+    """Seeded random layers (1-4 shards of random types and row counts, K up to 80 super-blocks,
+    M 1-600, default / tiny / odd wave targets): every descriptor row addresses a tile of its own
+    shard and valid output columns, GEMV rows partition each tile's k-range with counters and
+    partial slots inside the workspace (the split-K checker above), a one-record plan (bm = 1,
+    the kernel without a pipeline) gives every wave exactly one record, and GEMM rows cover each
+    tile exactly once over the whole k-range.  These are the bounds the kernels rely on."""
+    from gguf_hip import ops
+
+    rng = np.random.default_rng(2024)
+    for case in range(300):
+        K = 256 * int(rng.integers(1, 81))
+        shards, off = [], 0
+        for _ in range(int(rng.integers(1, 5))):
+            wt = int(rng.choice(G.ALL_TYPES))
+            n = int(rng.choice([rng.integers(1, 200), rng.integers(1, 40000)]))
+            shards.append((wt, n, off))
+            off += ops.tiles_bytes(wt, n, K)
+        M = int(rng.choice([rng.integers(1, 17), rng.integers(17, 601)]))
+        target = int(rng.choice([0, 0, 1, 16, int(rng.integers(2, 5000))]))
+        info, desc = ops.plan(shards, K, M, target)
+        d = _rows(desc)
+        nb, n_total = K // 256, sum(n for _, n, _ in shards)
+        tiles_of = {o: ((n + 63) // 64, n, wt) for wt, n, o in shards}
+        col_of, c = {}, 0
+        for wt, n, o in shards:
+            col_of[o] = c
+            c += n
+        assert d.shape[0] == info.n_desc and info.n_total == n_total and info.nb == nb, case
+        for row in d:
+            o = int(row[1]) | int(row[2]) << 32
+            ntile, n, wt = tiles_of[o]
+            t0, nt = int(row[3]), int(row[4])
+            assert row[0] == wt and 0 <= t0 and nt >= 1 and t0 + nt <= ntile, case
+            assert int(row[8]) == col_of[o] + 64 * t0, case
+            assert 1 <= int(row[9]) <= min(64 * nt, n - 64 * t0), case
+            assert 0 <= int(row[5]) < int(row[6]) <= nb, case
+        if info.form == 1:
+            assert M <= info.m_max and 1 <= info.nw <= 8, case
+            _check_gemv_rows(shards, K, info, desc)
+            assert all(int(r[11]) * 4 < info.ctr_bytes for r in d if r[12] > 1), case
+            if info.bm == 1:
+                assert all(int(r[6]) - int(r[5]) == info.nw for r in d), case
+            else:
+                assert all(int(r[6]) - int(r[5]) >= info.nw for r in d), case
+        else:
+            assert info.form == 2 and info.bm == (32 if M <= 32 else 64 if M <= 64 else 128 if M <= 128 else 256)
+            per = 4 if info.bm == 256 else 2
+            seen = {}
+            for row in d:
+                o, t0, nt = int(row[1]) | int(row[2]) << 32, int(row[3]), int(row[4])
+                assert nt <= per and (int(row[5]), int(row[6])) == (0, nb), case
+                for t in range(t0, t0 + nt):
+                    seen[(o, t)] = seen.get((o, t), 0) + 1
+            assert sorted(seen.values()) == [1] * sum(nt for nt, _, _ in tiles_of.values()), case
+
+
 def test_plan_descriptor_rows_mixed_layer():
     from gguf_hip import ops
 
