@@ -174,6 +174,31 @@ def test_graph_replay_matches_eager(dev):
         assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
 
 
+def test_random_layers_match_reference(dev):
+    """Seeded random layers through every form: 1-3 shards of random types (mixed layers
+    included) and row counts, K of 1-24 super-blocks, M across the GEMV buckets and the four
+    GEMM forms, default / tiny / large wave targets.  Each result is within 1e-2 of an fp32
+    matmul of the GPU-dequantized weights (pinned bit-exact by the dequant tests)."""
+    import gguf_hip
+    from gguf_hip.synth import random_shard
+
+    rng = np.random.default_rng(31)
+    for case in range(24):
+        K = 256 * int(rng.integers(1, 25))
+        shards = [(int(rng.choice(G.ALL_TYPES)), int(rng.integers(1, 1500))) for _ in range(int(rng.integers(1, 4)))]
+        M = int(rng.choice([1, 3, 5, 8, 12, 16, 20, 33, 64, 100, 129, 300]))
+        target = int(rng.choice([0, 1, 16, 4096]))
+        Ws = [random_shard(n, K, wt, dev, seed=100 * case + i) for i, (wt, n) in enumerate(shards)]
+        wf = torch.cat([gguf_hip.dequantize(W, wt, (n, K), torch.float32) for W, (wt, n) in zip(Ws, shards)])
+        gl = gguf_hip.pack_layer(Ws, [n for _, n in shards], [wt for wt, _ in shards], target_wgs=target)
+        x = _x(M, K, 5000 + case, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        ref = x.float() @ wf.T
+        scale = ref.abs().amax(dim=1, keepdim=True).clamp(min=1e-30)
+        err = float(((y.float() - ref).abs() / scale).amax())
+        assert err < TOL, (case, [(G.NAMES[wt], n) for wt, n in shards], K, M, target, err)
+
+
 def test_one_workspace_serves_every_form(dev):
     """One layer workspace across the GEMV (split tiles) and the three GEMM forms (stream-K
     partials) in an order where each form's partials would land on another form's counters if
