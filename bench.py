@@ -219,7 +219,7 @@ def main() -> int:
             gls[0].plans[gguf_hip.ops._pick_plan(gls[0].plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
                      "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
-                     "waves_per_wg": info.nw})
+                     "waves_per_wg": info.nw, "one_record": info.bm == 1})
         del g
     dom = max(rows, key=lambda r: r["us"])
     dom_wt = next(s[0] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
@@ -227,7 +227,9 @@ def main() -> int:
     # algorithmic bytes of one launch: packed weights + x (bf16) read once + y (bf16) written once
     dom_bytes = dom_w + 2 * M * dom["K"] + 2 * M * dom["N"]
     achieved = dom_bytes / (dom["us"] * 1e-6) / 1e9
-    dom_symbol = f"gqk::gemv_kernel<{dom['g']}, {dom_wt}>"
+    # the kernel's template arguments: token groups, type, and whether it is the build without the
+    # register pipeline (plans whose waves all stream one record)
+    dom_symbol = f"gqk::gemv_kernel<{dom['g']}, {dom_wt}, {'true' if dom['one_record'] else 'false'}>"
     traffic = _traffic(dom_symbol, dom, M)
     if args.detail:
         for r in rows:
