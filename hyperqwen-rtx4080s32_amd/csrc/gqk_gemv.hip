@@ -345,6 +345,21 @@ struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16
   static constexpr int BYTES = X + 24 * MPAD * 4;
 };
 
+// Order of the x slots in LDS.  An MFMA of token group g reads, in lane 4b + i, the 8 bytes of
+// token 4g + i at its slot.  Groups adjacent ([slot][i][g]): the G groups' operands of a lane are
+// one 8 G-byte run, a single ds_read_b128 at G = 2 (M = 8: IQ types 7-9% faster, Q4_K 3%, Q5_K 2%;
+// M = 16: up to 5%).  Tokens in order ([slot][t]): two 8-byte reads 32 bytes apart (ds_read2_b64);
+// kept for Q8_0 and Q5_0, whose one-record kernels measured 4-8% slower with the adjacent order
+// (more registers), and for Q6_K, whose G = 2 kernel sits at the three-waves register bound and
+// spilled with it.
+template <int T>
+constexpr bool x_groups_adjacent() { return T != GQK_Q8_0 && T != GQK_Q5_0 && T != GQK_Q6_K; }
+
+template <int MPAD, bool XG>
+__device__ __forceinline__ int x_slot(int slot, int t) {
+  return XG ? (slot * 4 + (t & 3)) * (MPAD / 4) + (t >> 2) : slot * MPAD + t;
+}
+
 // Issue the loads of super-block kb's x items (clamped addresses; masked when written).
 template <int MPAD>
 __device__ __forceinline__ void stage_load(const uint16_t* __restrict__ x, int64_t ldx, int M, int kb, int lane,
@@ -359,7 +374,7 @@ __device__ __forceinline__ void stage_load(const uint16_t* __restrict__ x, int64
   }
 }
 
-template <int MPAD, int FAM>
+template <int MPAD, int FAM, bool XG>
 __device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const uint4 (&v)[(8 * MPAD + 63) / 64][4]) {
   constexpr int NI = (8 * MPAD + 63) / 64;
   uint2* xs = (uint2*)wl;
@@ -379,7 +394,7 @@ __device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const 
       for (int j = 8; j < 16; ++j) b += bf2f(w[j] & 0xFFFF) + bf2f(w[j] >> 16);
       const bool live = t < M;
 #pragma unroll
-      for (int m = 0; m < 8; ++m) xs[(s32 * 8 + m) * MPAD + t] = live ? o[m] : make_uint2(0, 0);
+      for (int m = 0; m < 8; ++m) xs[x_slot<MPAD, XG>(s32 * 8 + m, t)] = live ? o[m] : make_uint2(0, 0);
       xsum16[(2 * s32) * MPAD + t] = live ? a : 0.f;
       xsum16[(2 * s32 + 1) * MPAD + t] = live ? b : 0.f;
       xsum32[s32 * MPAD + t] = live ? a + b : 0.f;
@@ -435,7 +450,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
         const int slot = s * MPS + m;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          v4s A = __builtin_bit_cast(v4s, xs[slot * MPAD + 4 * g + li]);
+          v4s A = __builtin_bit_cast(v4s, xs[x_slot<MPAD, x_groups_adjacent<T>()>(slot, 4 * g + li)]);
           C[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A, B, C[g], 0, 0, 0);
         }
       }
@@ -459,7 +474,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
     D r;
     stage_load<MPAD>(x, ldx, M, kw0, lane, xs);
     r.load(tbase + (int64_t)kw0 * (64 * D::REC), lane);
-    stage_store<MPAD, D::FAM>(wl, M, lane, xs);
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, M, lane, xs);
     process(r);
     return;
   }
@@ -492,7 +507,7 @@ __device__ __forceinline__ void gemv_pipeline(const uint8_t* __restrict__ tbase,
     r2.load(rec(kw0 + 2), lane);
   }
   auto step = [&](D& r, uint4 (&xv)[NI][4], int kb) {
-    stage_store<MPAD, D::FAM>(wl, M, lane, xv);
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, M, lane, xv);
     process(r);
     stage_load<MPAD>(x, ldx, M, min(kb + DEPTH, last), lane, xv);
     r.load(rec(kb + DEPTH), lane);
