@@ -355,8 +355,12 @@ struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16
 template <int T>
 constexpr bool x_groups_adjacent() { return T != GQK_Q8_0 && T != GQK_Q5_0 && T != GQK_Q6_K; }
 
+// G = 1 has a single group: there the adjacent pair is two consecutive slots of a token
+// ([slot / 2][t][slot % 2]), so two MFMAs' operands are one ds_read_b128 (M = 1-4: IQ types 5-9%
+// faster, Q4_K 2%).
 template <int MPAD, bool XG>
 __device__ __forceinline__ int x_slot(int slot, int t) {
+  if (XG && MPAD == 4) return ((slot >> 1) * 4 + t) * 2 + (slot & 1);
   return XG ? (slot * 4 + (t & 3)) * (MPAD / 4) + (t >> 2) : slot * MPAD + t;
 }
 
