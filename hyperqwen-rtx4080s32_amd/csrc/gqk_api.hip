@@ -37,8 +37,6 @@ int check_launch(const char* what) {
 constexpr int kDefaultTargetWaves = 2048;
 constexpr int kGemvWaves = 4;
 
-// bytes of the split-K arrival counters of `tiles` tiles (rounded to 256 so the partials stay aligned)
-int64_t gqk_counter_bytes(int64_t tiles) { return (tiles * 4 + 255) / 256 * 256; }
 // bytes of the fp32 split-K partials: [tile][split][64 rows][m_max tokens]
 int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return tiles * split * 64 * m_max * 4; }
 
@@ -50,7 +48,7 @@ extern "C" {
 
 const char* gqk_last_error(void) { return g_err.c_str(); }
 
-int gqk_version(void) { return 100; }
+int gqk_version(void) { return 200; }
 
 int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes) {
   const gqk_type* t = gqk_type_get(ggml_type);
@@ -89,6 +87,22 @@ int gqk_dequantize(const void* W, int64_t w_row_stride, int ggml_type, int64_t n
   int rc = gqk::launch_dequant(ggml_type, W, w_row_stride, n, K, out, ld_out, out_dtype, (hipStream_t)stream);
   if (rc) return fail(rc, "dequantize: type %d", ggml_type);
   return check_launch("dequantize");
+}
+
+int gqk_dequantize_tiles(const void* tiles, int ggml_type, int64_t n, int64_t K, void* out, int64_t ld_out,
+                         int out_dtype, void* stream) {
+  const gqk_type* t = gqk_type_get(ggml_type);
+  if (!t) return fail(GQK_ERR_TYPE, "unsupported GGML type %d", ggml_type);
+  if (n < 0 || K < 0 || K % 256 != 0)
+    return fail(GQK_ERR_SHAPE, "dequantize_tiles: K=%lld is not a multiple of 256", (long long)K);
+  if (out_dtype < 0 || out_dtype > 2) return fail(GQK_ERR_ARG, "dequantize_tiles: out_dtype %d", out_dtype);
+  if (n == 0 || K == 0) return GQK_OK;
+  if (!tiles || !out) return fail(GQK_ERR_ARG, "dequantize_tiles: null pointer");
+  if ((uintptr_t)tiles & 15) return fail(GQK_ERR_SHAPE, "dequantize_tiles: tiles must be 16-byte aligned");
+  if (ld_out < K) return fail(GQK_ERR_SHAPE, "dequantize_tiles: ld_out %lld < K %lld", (long long)ld_out, (long long)K);
+  int rc = gqk::launch_tile_dequant(ggml_type, tiles, n, K, out, ld_out, out_dtype, (hipStream_t)stream);
+  if (rc) return fail(rc, "dequantize_tiles: type %d, %lld x %lld", ggml_type, (long long)n, (long long)K);
+  return check_launch("dequantize_tiles");
 }
 
 int64_t gqk_tiles_bytes(int ggml_type, int64_t n, int64_t K) {
@@ -172,11 +186,12 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   };
   int64_t tiles = 0;
   for (int i = 0; i < nshards; ++i) tiles += (shards[i].n + 63) / 64;
-  // One counter region for every plan of the layer (the GEMV's per-tile split-K counters, the
-  // GEMM's stream-K workgroups), so that one workspace serves every M: no plan's partials
-  // overlap another plan's counters.
-  const int64_t ctr_bytes = std::max(gqk_counter_bytes(tiles), gqk_counter_bytes(GQK_GEMM_MAX_WGS));
-  if (ctr_bytes >= ((int64_t)1 << 31)) return fail(GQK_ERR_SHAPE, "plan: %lld tiles", (long long)tiles);
+  // The fixed counter region of every plan (the GEMV's split tiles and the GEMM's stream-K tiles
+  // index below GQK_CTR_WORDS), so that one workspace serves every layer and every M.
+  if (tiles > GQK_CTR_WORDS)
+    return fail(GQK_ERR_SHAPE, "plan: %lld 64-row tiles (%lld rows) above the %d the counter region serves",
+                (long long)tiles, (long long)(64 * tiles), GQK_CTR_WORDS);
+  const int64_t ctr_bytes = GQK_CTR_BYTES;
   pi.ctr_bytes = (int32_t)ctr_bytes;
   // The GEMV serves up to 16 rows; layers with a table type (IQ4_NL / IQ4_XS / IQ3_S, whose
   // lookups cost the GEMV the most per weight) switch to the 32-row GEMM above 8 rows, which
@@ -294,6 +309,11 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M) {
   return fail(GQK_ERR_FORM, "linear_workspace_bytes: unknown form %d", info->form);
 }
 
+int64_t gqk_workspace_bytes_max(void) {
+  const int64_t n = gqk::gemm_workspace_max();
+  return n < 0 ? fail(GQK_ERR_HIP, "workspace_bytes_max: no HIP device") : n;
+}
+
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
                int M, void* y, int64_t ldy, const void* bias, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!info) return fail(GQK_ERR_ARG, "linear: info is NULL");
@@ -314,7 +334,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     if (info->workspace_bytes > 0) {
       // counters at the start (one per split tile, fewer than the descriptor rows), partial slots after
       const int64_t cb = info->ctr_bytes, need = info->workspace_bytes;
-      if (cb <= 0 || (cb & 255) || need <= cb)
+      if (cb != GQK_CTR_BYTES || need <= cb)
         return fail(GQK_ERR_FORM, "linear: counter region %lld / workspace %lld bytes", (long long)cb, (long long)need);
       if (!workspace || workspace_bytes < need)
         return fail(GQK_ERR_SHAPE, "linear: workspace %lld bytes < %lld", (long long)workspace_bytes, (long long)need);

@@ -287,6 +287,23 @@ __device__ __forceinline__ void every_plane_word(int tid, F&& f) {
   }
 }
 
+// The 64 raw records of a chunk from its plane-major words (16-byte loads), into raw[row][REC] in LDS.
+template <int T>
+__device__ __forceinline__ void chunk_to_raw(const uint4* __restrict__ in, uint8_t* raw, int tid) {
+  constexpr int REC = gqk_planes<T>::v.rec;
+  auto scatter = [&](int wi, auto&& at) {
+    const uint4 q = in[wi];
+    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int r, b;
+      at(i, r, b);
+      raw[r * REC + b] = (uint8_t)(v[i >> 2] >> (8 * (i & 3)));
+    }
+  };
+  every_plane_word<T>(tid, scatter);
+}
+
 template <int T, bool TO_TILES, bool WIDE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
                                                      int64_t stride, int64_t n, int64_t nb) {
@@ -324,18 +341,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
     };
     every_plane_word<T>(tid, gather);
   } else {
-    const uint4* in = (const uint4*)(src + chunk * CB);
-    auto scatter = [&](int wi, auto&& at) {
-      const uint4 q = in[wi];
-      const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        int r, b;
-        at(i, r, b);
-        raw[r * REC + b] = (uint8_t)(v[i >> 2] >> (8 * (i & 3)));
-      }
-    };
-    every_plane_word<T>(tid, scatter);
+    chunk_to_raw<T>((const uint4*)(src + chunk * CB), raw, tid);
     __syncthreads();
     uint8_t* rows = dst + row0 * stride + kb * REC;
     if (WIDE) {
@@ -380,6 +386,77 @@ int launch_repack(int type, const void* W, int64_t stride, int64_t n, int64_t K,
   uint8_t* d = (uint8_t*)(to_tiles ? tiles : W);
   switch (type) {
 #define C(T) case T: launch_repack_t<T>(to_tiles, wide, grid, st, s, d, stride, n, nb); return GQK_OK;
+    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
+  }
+  return GQK_ERR_TYPE;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Dequantize straight from the tiles: one workgroup per chunk (tile t, super-block kb) gathers the
+// chunk's planes back into its 64 raw records in LDS (as the unrepack does), then every thread
+// decodes (row, 32-weight group) items from LDS with the same deq32 as the raw-row dequantizer
+// and writes them to the output row: each tile byte is read once, no raw-row temporary.
+template <int T, typename O, bool VEC>
+__global__ __launch_bounds__(256) void tile_dequant_kernel(const uint8_t* __restrict__ tiles, int64_t n, int64_t nb,
+                                                           O* __restrict__ out, int64_t ldo) {
+  constexpr int REC = gqk_planes<T>::v.rec, CB = 64 * REC;
+  __shared__ __attribute__((aligned(16))) uint8_t raw[CB + 16];
+  const int tid = threadIdx.x;
+  const int64_t chunk = blockIdx.x, kb = chunk % nb, tile = chunk / nb;
+  chunk_to_raw<T>((const uint4*)(tiles + chunk * CB), raw, tid);
+  __syncthreads();
+  for (int it = tid; it < 64 * 8; it += 256) {   // consecutive threads: consecutive groups of a row
+    const int r = it >> 3, g = it & 7;
+    const int64_t row = tile * 64 + r;
+    if (row >= n) continue;
+    float w[32];
+    deq32<T>(raw + r * REC, g, w);
+    O* o = out + row * ldo + kb * 256 + g * 32;
+    if constexpr (VEC) {
+      constexpr int PER = 16 / sizeof(O);
+      uint4* ov = (uint4*)o;
+#pragma unroll
+      for (int v = 0; v < 32 / PER; ++v) {
+        O c[PER];
+#pragma unroll
+        for (int j = 0; j < PER; ++j) c[j] = cvt_out<O>(w[v * PER + j]);
+        ov[v] = __builtin_bit_cast(uint4, c);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) o[j] = cvt_out<O>(w[j]);
+    }
+  }
+}
+
+template <int T>
+static int launch_tile_dequant_t(const void* tiles, int64_t n, int64_t K, void* out, int64_t ldo, int dtype,
+                                 hipStream_t st) {
+  const int64_t nb = K / 256, chunks = (n + 63) / 64 * nb;
+  if (chunks == 0) return GQK_OK;
+  if (chunks >= ((int64_t)1 << 31)) return GQK_ERR_SHAPE;
+  const dim3 grid((unsigned)chunks), block(256);
+  const int esz = dtype == 0 ? 4 : 2;
+  const bool vec = ((uintptr_t)out % 16 == 0) && ((ldo * esz) % 16 == 0);
+  const uint8_t* t = (const uint8_t*)tiles;
+#define L(O, V) hipLaunchKernelGGL((tile_dequant_kernel<T, O, V>), grid, block, 0, st, t, n, nb, (O*)out, ldo)
+  if (dtype == 0) {
+    if (vec) L(float, true); else L(float, false);
+  } else if (dtype == 1) {
+    if (vec) L(__bf16, true); else L(__bf16, false);
+  } else {
+    if (vec) L(_Float16, true); else L(_Float16, false);
+  }
+#undef L
+  return GQK_OK;
+}
+
+int launch_tile_dequant(int type, const void* tiles, int64_t n, int64_t K, void* out, int64_t ldo, int dtype,
+                        hipStream_t st) {
+  switch (type) {
+#define C(T) case T: return launch_tile_dequant_t<T>(tiles, n, K, out, ldo, dtype, st);
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C

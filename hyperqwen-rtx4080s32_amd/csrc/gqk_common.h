@@ -123,7 +123,12 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 // descriptor row of a grouped launch (int32 words)
 #define GQK_DESC_WORDS 16
 #define GQK_SPLIT_MAX 16   // split-K factor bound: the last workgroup loads every partial at once
-#define GQK_GEMM_MAX_WGS 1024   // persistent GEMM workgroups (up to three per CU) a launch may use: the counter region
+#define GQK_GEMM_MAX_WGS 1024   // persistent GEMM workgroups (up to three per CU) a launch may use
+// Arrival counters at the start of every workspace: one fixed region for every plan of every
+// layer (GEMV split tiles and GEMM stream-K tiles each index below it), so that one workspace per
+// device serves all layers and batch sizes: no plan's fp32 partials overlap another's counters.
+#define GQK_CTR_BYTES 262144   // (mirrored in include/gguf_hip.h)
+#define GQK_CTR_WORDS (GQK_CTR_BYTES / 4)
 #ifndef GQK_GEMV_MAX_M
 #define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form (8 for layers with an IQ type); the GEMM above
 #endif

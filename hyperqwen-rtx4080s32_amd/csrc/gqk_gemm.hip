@@ -805,6 +805,18 @@ int64_t gemm_workspace(int bm, int n_desc, int M, int nb, int64_t ctr_bytes) {
   return ctr_bytes + (R + gsk - 1) * gb_slot_floats(bm) * 4;
 }
 
+// Any M: the remainder tiles R <= G - 1 and the stream-K workgroups gsk <= G, so R + gsk - 1 <=
+// 2 G - 2 partial slots of the form's tile.
+int64_t gemm_workspace_max() {
+  int64_t m = 0;
+  for (int bm : {32, 64, 128, 256}) {
+    const int G = gb_workgroups(bm);
+    if (G <= 0) return -1;
+    m = std::max<int64_t>(m, (int64_t)(2 * G - 2) * gb_slot_floats(bm) * 4);
+  }
+  return GQK_CTR_BYTES + m;
+}
+
 template <class GE>
 static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const uint8_t* packed, const int32_t* desc,
                      const uint16_t* x, int64_t ldx, uint16_t* y, int64_t ldy, const uint16_t* bias,

@@ -91,12 +91,19 @@ def ggml_dequantize(W: torch.Tensor, quant_type: int, m: int, n: int, dtype: tor
     if dtype not in _DTYPES:
         raise ValueError(f"ggml_dequantize: dtype {dtype}")
     W = _rows_view(W, "ggml_dequantize")
+    # the shape contract first (the C side only sees a row stride, so a view narrower than the
+    # rows' bytes would read past its last row)
+    if m > 0 and n > 0:
+        if W.shape[0] < m:
+            raise ValueError(f"ggml_dequantize: {W.shape[0]} rows < m={m}")
+        bw, bb, _, _ = type_info(quant_type)
+        if n % bw or W.shape[1] < n // bw * bb:
+            raise ValueError(f"ggml_dequantize: rows of {W.shape[1]} bytes do not hold {n} weights of type "
+                             f"{quant_type} ({bw}-weight blocks of {bb} bytes)")
     _require_gpu(W, "ggml_dequantize")
     out = torch.empty((m, n), dtype=dtype, device=W.device)
     if m == 0 or n == 0:
         return out
-    if W.shape[0] < m:
-        raise ValueError(f"ggml_dequantize: {W.shape[0]} rows < m={m}")
     check(lib.gqk_dequantize(ctypes.c_void_p(W.data_ptr()), W.stride(0), int(quant_type), m, n,
                              ctypes.c_void_p(out.data_ptr()), out.stride(0), _DTYPES[dtype], _stream(W.device)),
           "ggml_dequantize")
@@ -137,9 +144,19 @@ def unrepack_tiles(tiles: torch.Tensor, n_out: int, K: int, weight_type: int) ->
 
 
 def dequantize_tiles(tiles: torch.Tensor, n_out: int, K: int, weight_type: int, dtype=torch.bfloat16) -> torch.Tensor:
-    """The tiles' weights [n_out, K] (un-repack, then the dequantizer; as the reference's
-    dequantize_tiles, gguf-plugin/gluon/tiles.py:141-149)."""
-    return dequantize(unrepack_tiles(tiles, n_out, K, weight_type), weight_type, (n_out, K), dtype)
+    """The tiles' weights [n_out, K], decoded straight from the tile layout in one pass (the
+    reference's dequantize_tiles / dequantize_iq3s_tiles, gguf-plugin/gluon/tiles.py:141-149,
+    gguf-plugin/gluon/iq3s_tile_dequant.py:22-63): the same bits as dequantize of the raw rows."""
+    _require_gpu(tiles, "dequantize_tiles")
+    if dtype not in _DTYPES:
+        raise ValueError(f"dequantize_tiles: dtype {dtype}")
+    if tiles.dtype != torch.uint8 or not tiles.is_contiguous() or tiles.numel() < tiles_bytes(weight_type, n_out, K):
+        raise ValueError("dequantize_tiles: tiles must be a contiguous uint8 buffer of the shard's tile bytes")
+    out = torch.empty((n_out, K), dtype=dtype, device=tiles.device)
+    check(lib.gqk_dequantize_tiles(ctypes.c_void_p(tiles.data_ptr()), int(weight_type), n_out, K,
+                                   ctypes.c_void_p(out.data_ptr()), out.stride(0), _DTYPES[dtype], _stream(tiles.device)),
+          "dequantize_tiles")
+    return out
 
 
 # ----------------------------------------------------------------------------------------------
@@ -168,13 +185,34 @@ class GroupedLayer:
     K: int
     descs: list[torch.Tensor] = field(default_factory=list)
     plans: list[int] = field(default_factory=list)    # flattened GqkPlanInfo tuples, one per bucket
-    # split-K workspace of the GEMV plans: arrival counters (zeroed once here, left zero by every
-    # launch) and fp32 partials; calls on one layer must not overlap in time
+    # the device's shared split-K / stream-K workspace (device_workspace): arrival counters (zero at
+    # rest, left zero by every launch) and fp32 partials; calls sharing it must not overlap in time
     workspace: torch.Tensor | None = None
 
     @property
     def n_total(self) -> int:
         return sum(self.n_outs)
+
+
+# one workspace per device, shared by every grouped layer prepared on it
+_WORKSPACES: dict[int, torch.Tensor] = {}
+
+
+def device_workspace(device: torch.device, need: int = 0) -> torch.Tensor:
+    """The device's shared workspace: zero-filled int32, at least ``gqk_workspace_bytes_max()``
+    bytes (every GEMM plan at any M) and ``need`` (a layer's GEMV plans).  It is made at a layer's
+    preparation and never resized or freed while a layer holds it, so the apply path allocates
+    nothing and a captured graph's pointer stays valid.  Only a layer whose GEMV plans need more
+    (a very large custom wave target) gets a larger one, which then serves the layers prepared
+    after it; earlier layers keep theirs."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACES.get(idx)
+    if ws is None or ws.numel() * ws.element_size() < need:
+        with torch.cuda.device(idx):
+            size = max(need, check(lib.gqk_workspace_bytes_max(), "workspace_bytes_max"))
+        ws = torch.zeros((size + 3) // 4, dtype=torch.int32, device=torch.device("cuda", idx))
+        _WORKSPACES[idx] = ws
+    return ws
 
 
 def prepare_grouped_layer(tiles_list: list[torch.Tensor], n_outs: list[int], wtypes: list[int], K: int,
@@ -208,7 +246,7 @@ def grouped_layer_from_packed(packed: torch.Tensor, n_outs: list[int], wtypes: l
         gl.descs.append(desc.to(packed.device))
         gl.plans.extend(info.as_tuple())
         ws = max(ws, info.workspace_bytes)
-    gl.workspace = torch.zeros(max(ws, 256) // 4, dtype=torch.int32, device=packed.device)
+    gl.workspace = device_workspace(packed.device, ws)
     return gl
 
 
@@ -281,35 +319,24 @@ def fused_mul_mat_gguf_grouped_out(x: torch.Tensor, packed: torch.Tensor, descs:
     _grouped_into(x, packed, descs, plans, workspace, bias, out)
 
 
-def _ensure_workspace(gl: GroupedLayer, M: int) -> None:
-    """Grow the layer's workspace (zero-filled, as the counters need) to what the plan serving M
-    rows needs.  GEMV plans are covered at preparation; the large-M GEMM's stream-K partials
-    depend on M, so the first call at a larger M grows it (outside any graph capture)."""
-    if M <= 0:
-        return
-    i = _pick_plan(gl.plans, M)
-    info = GqkPlanInfo.from_tuple(gl.plans[i * _NPLAN:(i + 1) * _NPLAN])
-    need = check(lib.gqk_linear_workspace_bytes(ctypes.byref(info), M), "linear_workspace_bytes")
-    have = gl.workspace.numel() * gl.workspace.element_size()
-    if need > have:
-        gl.workspace = torch.zeros((need + 3) // 4, dtype=torch.int32, device=gl.packed.device)
-
-
 def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None = None,
-                    out: torch.Tensor | None = None) -> torch.Tensor:
+                    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """y = x @ W^T (+ bias) for a prepared grouped layer, in x's dtype.  The kernels take bf16
     activations; other floating dtypes are rounded to bf16 on the way in and the bf16 result
     is cast back.  A bf16 bias [n_total] is fused into the kernel's epilogue; a bias of another
     dtype is added afterwards in that dtype (as the reference's out.add_(bias)).  out: a bf16
     [M, n_total] view with unit column stride (a column slice of a wider output) to write
-    into, for bf16 x; it is returned."""
+    into, for bf16 x; it is returned.  workspace: a zero-filled int32 buffer of at least
+    ``gqk_workspace_bytes_max()`` bytes to use instead of the device's shared one (calls that may
+    overlap in time on different streams each need their own).  Nothing is allocated here
+    besides the output."""
     _require_gpu(x, "mul_mat_grouped")
     if x.dim() != 2 or x.shape[1] != gl.K:
         raise ValueError(f"mul_mat_grouped: x {tuple(x.shape)} does not match K={gl.K}")
     xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
     if xb.stride(1) != 1 or xb.stride(0) % 8 or xb.data_ptr() % 16:
         xb = xb.contiguous()
-    _ensure_workspace(gl, int(xb.shape[0]))
+    ws = gl.workspace if workspace is None else workspace
     fused = None
     if bias is not None:
         if bias.shape != (gl.n_total,) or bias.device != x.device:
@@ -321,21 +348,57 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
                 or out.device != x.device or (out.numel() and out.stride(1) != 1)):
             raise ValueError(f"mul_mat_grouped: out must be a bf16 [{xb.shape[0]}, {gl.n_total}] view with unit "
                              f"column stride on {x.device}, for bf16 x")
-        fused_mul_mat_gguf_grouped_out(xb, gl.packed, gl.descs, gl.plans, gl.workspace, out, fused)
+        fused_mul_mat_gguf_grouped_out(xb, gl.packed, gl.descs, gl.plans, ws, out, fused)
         if bias is not None and fused is None:
             out.add_(bias)
         return out
-    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, gl.workspace, fused)
+    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, ws, fused)
     y = y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     if bias is not None and fused is None:
         y.add_(bias)
     return y
 
 
+_CACHE_ATTR = "_gguf_hip_layers"
+
+
+def cached_layer(weight: torch.Tensor, weight_type: int, n_out: int, kind: str = "rows") -> GroupedLayer:
+    """The grouped layer of a weight given as raw GGUF rows (kind "rows", any row stride) or as one
+    shard's tiles ("tiles"), made on the first call and kept in a dict attached to the weight's base
+    tensor (the storage the view belongs to, e.g. a layer parameter), so it goes with that storage
+    and a freed weight's entry can never serve another (the reference keys its caches by the
+    layer's own metadata for that reason, gguf-plugin/gluon/tiles_grouped.py:271-275).  The key is
+    the view's offset, shape, strides, type and rows, and the entry is rebuilt when the base's
+    version counter shows an in-place write.  Later calls allocate nothing and copy nothing."""
+    base = weight._base if weight._base is not None else weight
+    key = (kind, weight.storage_offset(), tuple(weight.shape), tuple(weight.stride()), int(weight_type), int(n_out),
+           str(weight.device))
+    cache = getattr(base, _CACHE_ATTR, None)
+    if cache is None:
+        cache = {}
+        setattr(base, _CACHE_ATTR, cache)
+    hit = cache.get(key)
+    if hit is not None and hit[0] == base._version:
+        return hit[1]
+    if kind == "rows":
+        gl = pack_layer([weight], [n_out], [weight_type])
+    elif kind == "tiles":
+        per_row = weight.numel() // (-(-n_out // 64) * 64)
+        rec = type_info(weight_type)[2]
+        if per_row % rec:
+            raise ValueError(f"cached_layer: {weight.numel()} tile bytes do not hold {n_out} rows of type {weight_type}")
+        flat = weight.reshape(-1) if weight.is_contiguous() else weight.contiguous().reshape(-1)
+        gl = grouped_layer_from_packed(flat, [n_out], [weight_type], per_row // rec * 256)
+    else:
+        raise ValueError(f"cached_layer: kind {kind!r}")
+    cache[key] = (base._version, gl)
+    return gl
+
+
 def fused_mul_mat_gguf(x: torch.Tensor, qweight: torch.Tensor, qweight_type: int) -> torch.Tensor:
     """The plugin's module-level op on raw rows (``_fused_mul_mat_gguf``,
-    gguf-plugin/patches/gguf-prefill-dispatch.patch:9-50): y = x @ W^T.  Unprepared raw rows are
-    repacked for this call (the loader's prepare step does it once instead)."""
+    gguf-plugin/patches/gguf-prefill-dispatch.patch:9-50): y = x @ W^T.  The first call on a weight
+    repacks and plans it (``cached_layer``); later calls reuse that and allocate only the output."""
     if qweight_type in UNQUANTIZED_TYPES:
         return x @ (qweight if qweight.dtype == x.dtype else qweight.to(x.dtype)).T
     if qweight_type not in GGUF_TYPES:
@@ -343,5 +406,4 @@ def fused_mul_mat_gguf(x: torch.Tensor, qweight: torch.Tensor, qweight_type: int
     n = qweight.shape[0]
     if x.shape[0] == 0:
         return torch.empty((0, n), dtype=x.dtype, device=x.device)
-    gl = pack_layer([qweight], [n], [qweight_type])
-    return mul_mat_grouped(x, gl)
+    return mul_mat_grouped(x, cached_layer(qweight, qweight_type, n, "rows"))

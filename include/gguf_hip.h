@@ -31,6 +31,8 @@ extern "C" {
 #define GQK_FORM_GEMV 1 /* M <= 16 (<= 8 with an IQ shard): in-register decode GEMV (MFMA 4x4x4 per scale group) */
 #define GQK_FORM_GEMM 2 /* above: LDS-dequant bf16 MFMA GEMM (any M) */
 
+#define GQK_CTR_BYTES 262144 /* the arrival-counter region at the start of every workspace */
+
 #define GQK_DTYPE_F32 0
 #define GQK_DTYPE_BF16 1
 #define GQK_DTYPE_F16 2
@@ -55,8 +57,8 @@ typedef struct gqk_plan_info {
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
   int32_t nb;         /* K / 256 */
   int32_t nw;         /* GEMV: waves per workgroup (they split the workgroup's k-range) */
-  int32_t ctr_bytes;  /* bytes of arrival counters at the start of the workspace; the same in every
-                         plan of one layer, so one workspace serves all of them */
+  int32_t ctr_bytes;  /* bytes of arrival counters at the start of the workspace: GQK_CTR_BYTES in
+                         every plan, so one workspace serves every layer and every M */
   int64_t n_total;    /* output columns: sum of the shards' rows */
   int64_t workspace_bytes; /* device workspace gqk_linear needs (any M <= m_max) */
 } gqk_plan_info;
@@ -79,6 +81,13 @@ int gqk_type_info(int ggml_type, int32_t* info, int32_t* planes);
  * (gguf-plugin/patches/gguf-prefill-dispatch.patch:42-45, gguf-plugin/gluon/tiles.py:147-149). */
 int gqk_dequantize(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, int64_t K, void* out,
                    int64_t ld_out, int out_dtype, void* stream);
+
+/* Dequantize n rows of K weights straight from the tile layout (gqk_repack's output) into
+ * out[n, ld_out] of out_dtype, in one pass (no raw-row temporary); the same bits as
+ * gqk_dequantize of the raw rows.  Replaces dequantize_tiles / dequantize_iq3s_tiles
+ * (gguf-plugin/gluon/tiles.py:141-149, gguf-plugin/gluon/iq3s_tile_dequant.py:22-63). */
+int gqk_dequantize_tiles(const void* tiles, int ggml_type, int64_t n, int64_t K, void* out, int64_t ld_out,
+                         int out_dtype, void* stream);
 
 /* Bytes of the tile layout of an n x K shard (< 0: error code).  K % 256 == 0. */
 int64_t gqk_tiles_bytes(int ggml_type, int64_t n, int64_t K);
@@ -106,15 +115,21 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
  * partial tiles, which depends on M and on the current device's CU count.  Replaces the reference's transient split-K partials (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
 int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
 
+/* Workspace bytes that serve every GEMM plan at any M on the current device (< 0: error): one
+ * buffer of this size (or of a layer's GEMV workspace_bytes, if larger) serves every layer on the
+ * device, as calls on one stream never overlap.  No counterpart in the reference, whose split-K
+ * partials are transient torch tensors (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
+int64_t gqk_workspace_bytes_max(void);
+
 /* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T (+ bias) over the grouped layer's shards (columns in
  * shard order), on `stream`.  bias: NULL or bf16 [info->n_total] device memory, added in fp32
  * before the single rounding to bf16 (the reference adds it afterwards with out.add_(bias),
  * gguf-plugin/patches/gguf-tiles-grouped.patch:167-168).  desc_dev: the plan's descriptor table in device memory.  workspace: at
  * least gqk_linear_workspace_bytes(info, M) bytes of 256-byte aligned device memory (NULL when
- * that is 0) holding arrival counters (its first info->ctr_bytes bytes) and fp32 partials (after
+ * that is 0) holding arrival counters (its first GQK_CTR_BYTES bytes) and fp32 partials (after
  * them); it must be zero-filled before its first use, every launch leaves the counters at zero
- * again, one workspace serves every plan of one layer (any M: the counter region is the same in
- * all of them), and launches sharing one workspace must not overlap in time.  M must be <= info->m_max.  Replaces the grouped op
+ * again, one workspace serves every plan of every layer (the counter region is the same in all
+ * of them), and launches sharing one workspace must not overlap in time.  M must be <= info->m_max.  Replaces the grouped op
  * torch.ops.vllm._fused_mul_mat_gguf_tiles_grouped -> gluon_mul_mat_tiles_grouped
  * (gguf-plugin/patches/gguf-tiles-grouped.patch:28-72, gguf-plugin/gluon/interface.py:141-188). */
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,

@@ -104,7 +104,7 @@ def _check_gemv_rows(shards, K, info, desc):
 
 
 def test_plan_gemv_balanced_split_partition():
-    from gguf_hip import ops
+    from gguf_hip import _lib, ops
 
     for target in (1, 16, 97, 1024, 4096, 0):
         info, desc = ops.plan([(21, 6144, 0)], 20 * 256, 1, target)
@@ -115,8 +115,8 @@ def test_plan_gemv_balanced_split_partition():
         if S > 1:
             assert nw == 4                                  # K splits across workgroups only past a full one
         assert set(ncs.values()) == {S}                     # 96 tiles: one round or whole rounds, no tail
-        # the counter region: one int per tile, at least the GEMM's 1024 workgroups, 256-byte rounded
-        assert info.ctr_bytes == 4096
+        # the counter region: the fixed GQK_CTR_BYTES of every plan
+        assert info.ctr_bytes == _lib.GQK_CTR_BYTES
     assert ops.plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
     info = ops.plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
     assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
@@ -224,7 +224,7 @@ def test_plan_random_layers_stay_in_bounds():
 
 
 def test_plan_descriptor_rows_mixed_layer():
-    from gguf_hip import ops
+    from gguf_hip import _lib, ops
 
     K = 3 * 256
     off2 = ops.tiles_bytes(21, 70, K)
@@ -232,10 +232,13 @@ def test_plan_descriptor_rows_mixed_layer():
     d = _rows(desc)
     assert info.types_mask == 0 and info.n_total == 370 and info.g == 2
     assert info.split == 1 and info.workspace_bytes == 0
-    # one counter region for every plan of a layer, so one workspace serves every M
-    for shards, k in (([(21, 70, 0), (12, 300, off2)], K), ([(12, 70000, 0)], 512)):
+    # one counter region for every plan of every layer, so one workspace serves every layer and M
+    for shards, k in (([(21, 70, 0), (12, 300, off2)], K), ([(12, 70000, 0)], 512), ([(12, 64 * 65536, 0)], 256)):
         regions = {ops.plan(shards, k, m, t)[0].ctr_bytes for m in (1, 8, 16, 17, 100, 2048) for t in (0, 1, 4096)}
-        assert regions == {max(4096, ((sum((n + 63) // 64 for _, n, _ in shards) * 4 + 255) // 256) * 256)}
+        assert regions == {_lib.GQK_CTR_BYTES}
+    # a layer with more tiles than the region has counters is refused, not silently overrun
+    with pytest.raises(ValueError, match="counter region"):
+        ops.plan([(12, 64 * 65536 + 1, 0)], 256, 8)
     # one workgroup per tile: IQ3_S 2 tiles (64 + 6 rows), Q4_K 5 tiles (4 x 64 + 44)
     assert d[:, 0].tolist() == [21, 21, 12, 12, 12, 12, 12]
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
@@ -275,3 +278,42 @@ def test_plan_buckets():
     assert ops.plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 2
     for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
         assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm
+
+
+def test_ggml_dequantize_rejects_rows_narrower_than_n():
+    """A column-offset view whose rows hold fewer bytes than n weights need is a ValueError before
+    any launch (the C side sees only the row stride, so it would read past the last row)."""
+    import torch
+
+    from gguf_hip import ops
+
+    W = torch.zeros((4, 2 * 144), dtype=torch.uint8)            # two Q4_K blocks per row
+    with pytest.raises(ValueError, match="do not hold"):
+        ops.ggml_dequantize(W[:, 16:16 + 144], 12, 4, 512)      # 144 bytes for 512 weights
+    with pytest.raises(ValueError, match="do not hold"):
+        ops.ggml_dequantize(W, 12, 4, 300)                      # not whole blocks
+    with pytest.raises(ValueError, match="rows"):
+        ops.ggml_dequantize(W, 12, 5, 512)
+    with pytest.raises(NotImplementedError):
+        ops.ggml_dequantize(W, 16, 4, 256)                      # IQ2_XXS: no kernel
+    with pytest.raises(ValueError, match="GPU"):
+        ops.ggml_dequantize(W, 12, 4, 512)                      # the shape is fine: CPU tensors have no path
+
+
+def test_interface_names_resolve_for_the_plugin():
+    """The plugin's import lines (gguf-plugin/patches/gguf-gluon-dispatch.patch:13 and the later
+    patches' additions) resolve against gguf_hip.interface, with the reference's meanings."""
+    from gguf_hip import interface as I
+    from gguf_hip import ops
+
+    ns = {}
+    exec("from gguf_hip.interface import GLUON_MAX_ROWS, GLUON_TYPES, gluon_mul_mat", ns)
+    exec("from gguf_hip.interface import (GLUON_MAX_ROWS, GLUON_TYPES, GLUON_TILE_TYPES, gluon_mul_mat, "
+         "gluon_mul_mat_iq3s_tiles, gluon_mul_mat_tiles, gluon_mul_mat_tiles_grouped, prepare_grouped_layer, "
+         "repack_iq3s_tiles, repack_tiles, dequantize_tiles, dequantize_iq3s_tiles)", ns)
+    assert ns["GLUON_MAX_ROWS"] == 16
+    assert ns["GLUON_TYPES"] == frozenset(ops.GGUF_TYPES) == I.GLUON_TILE_TYPES
+    assert {I.GGML_TYPE_Q2_K, I.GGML_TYPE_Q4_K, I.GGML_TYPE_IQ3_S, I.GGML_TYPE_IQ4_XS} == {10, 12, 21, 23}
+    import torch
+    with pytest.raises(NotImplementedError):
+        I.gluon_mul_mat(torch.zeros((1, 256), dtype=torch.bfloat16), torch.zeros((1, 66), dtype=torch.uint8), 16, 1)

@@ -33,6 +33,25 @@ def test_dequantize_bit_exact(dev, wt):
     assert g16.dtype == torch.float16 and torch.equal(g16.cpu(), ref_t.to(torch.float16))
 
 
+@pytest.mark.parametrize("wt", [G.Q8_0, G.Q3_K, G.Q5_K, G.Q6_K], ids=lambda t: G.NAMES[t])
+def test_dequantize_golden_kq_ref_rows(dev, wt):
+    """The reference's own dequantization vectors (gguf-plugin/gluon/kq_ref.py, written to
+    tests/golden/kq_ref_*.npz) straight through gqk_dequantize: no oracle in between."""
+    import os
+
+    import gguf_hip
+
+    d = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"kq_ref_{wt}.npz"))
+    raw, w = d["raw"], d["w"]
+    n, K = w.shape
+    got = gguf_hip.dequantize(_to_dev(raw, dev), wt, (n, K), torch.float32).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), w.view(np.uint32))
+    # and through the tiles: repack, then the one-pass tile dequantizer
+    tiles = gguf_hip.repack_tiles(_to_dev(raw, dev), n, wt)
+    got_t = gguf_hip.dequantize_tiles(tiles, n, K, wt, torch.float32).cpu().numpy()
+    assert np.array_equal(got_t.view(np.uint32), w.view(np.uint32))
+
+
 @pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
 def test_dequantize_strided_rows_and_quantized_weights(dev, wt):
     import gguf_hip

@@ -144,6 +144,45 @@ def test_iq4xs_is_iq4nl_per_subblock():
         assert np.array_equal(G.dequantize(xs[None], G.IQ4_XS)[0], expect.astype(np.float32)), ls
 
 
+def _iq4xs_encode(d, ls8, nib256):
+    """IQ4_XS block from chosen fields, written from the prose of gguf-plugin/gluon/iq4xs.py:5-11
+    (not from the oracle's decode): d f16 | scales_h u16 | scales_l u8[4] | qs u8[128].  The
+    6-bit scale of sub-block ib: its low 4 bits are nibble ib of scales_l (byte ib // 2, low nibble
+    for even ib), its high 2 bits are bits 2 ib, 2 ib + 1 of scales_h.  Weight j < 16 of
+    sub-block ib is the low nibble of qs byte 16 ib + j, weight 16 + j the high nibble."""
+    blk = np.zeros(136, np.uint8)
+    blk[0:2] = f16b(d)
+    sh = 0
+    for ib in range(8):
+        ls = int(ls8[ib])
+        blk[4 + ib // 2] |= (ls & 0xF) << (4 * (ib % 2))
+        sh |= (ls >> 4) << (2 * ib)
+        for j in range(16):
+            blk[8 + 16 * ib + j] = int(nib256[32 * ib + j]) | (int(nib256[32 * ib + 16 + j]) << 4)
+    blk[2:4] = np.array([sh], np.uint16).view(np.uint8)
+    return blk
+
+
+def test_iq4xs_known_block_distinct_subscales():
+    """Eight different 6-bit sub-scales, so a decode that takes a sub-block's scale from another
+    sub-block's nibble (e.g. scales_l[ib % 4] >> 4 * (ib // 4)) or bit pair fails."""
+    ls = np.array([1, 62, 17, 40, 5, 33, 48, 26])
+    rng = np.random.default_rng(12)
+    for d in (1.0, float(np.float16(3.0517578e-4)), float(np.float16(-0.0123))):
+        nib = rng.integers(0, 16, 256)
+        w = G.dequantize(_iq4xs_encode(d, ls, nib)[None], G.IQ4_XS)[0]
+        expect = np.repeat(np.float64(d) * (ls - 32), 32) * IQ4_KVALUES[nib].astype(np.float64)
+        assert np.array_equal(w, expect.astype(np.float32))
+    # one non-zero nibble field at a time: each sub-block's scale is found in its own fields only
+    for ib in range(8):
+        one = np.zeros(8, np.int64)
+        one[ib] = ls[ib]
+        nib = np.full(256, 9)                                   # kvalue 13 everywhere
+        w = G.dequantize(_iq4xs_encode(1.0, one, nib)[None], G.IQ4_XS)[0].reshape(8, 32)
+        for jb in range(8):
+            assert np.all(w[jb] == np.float32((one[jb] - 32) * 13)), (ib, jb)
+
+
 def _iq3s_encode(d, scales8, idx32, signs256):
     """IQ3_S block from chosen fields: 8 sub-block scales (4 bit), 32 grid indices (9 bit, one
     per 4 weights in order), 256 sign bits.  Scatter encoder of the GGML layout: index i of
