@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <vector>
 #include "gguf_hip.h"
@@ -39,6 +40,45 @@ constexpr int kGemvWaves = 4;
 
 // bytes of the fp32 split-K partials: [tile][split][64 rows][m_max tokens]
 int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return tiles * split * 64 * m_max * 4; }
+
+// ---- the no-allocation entry point's workspace -------------------------------------------------
+// A file-scope device array, one copy per GPU the library runs on (held until the process ends):
+// the arrival counters (GQK_CTR_BYTES, zero at rest) then room for the fp32 split-K / stream-K
+// partials.  Host code never uses the array's name as an address: the per-device address comes
+// from hipGetSymbolAddress, taken once per device with that device current.
+constexpr int64_t kScratchBytes = GQK_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {nullptr};
+
+__global__ void zero_words(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+// The current device's scratch address; the first call on a device takes it and clears the
+// counter region with a fill kernel on `st` (no memset: the call may be under graph capture, where
+// the fill is recorded too and then zeroes counters that are zero at rest anyway).
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(GQK_ERR_HIP, "linear_noalloc: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(GQK_ERR_HIP, "linear_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    if ((uintptr_t)ptr & 255) return fail(GQK_ERR_HIP, "linear_noalloc: scratch on device %d not 256-byte aligned", dev);
+    hipLaunchKernelGGL(zero_words, dim3(64), dim3(256), 0, st, (uint32_t*)ptr, (int64_t)GQK_CTR_BYTES / 4);
+    const hipError_t le = hipGetLastError();
+    if (le != hipSuccess) return fail(GQK_ERR_HIP, "linear_noalloc: clearing the scratch counters: %s", hipGetErrorString(le));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GQK_OK;
+}
 
 }  // namespace
 
@@ -360,6 +400,25 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     return check_launch("linear (GEMM)");
   }
   return fail(GQK_ERR_FORM, "linear: unknown form %d", info->form);
+}
+
+int gqk_linear_noalloc(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x,
+                       int64_t ldx, int M, void* y, int64_t ldy, const void* bias, void* stream) {
+  if (!info) return fail(GQK_ERR_ARG, "linear_noalloc: info is NULL");
+  if (M < 0) return fail(GQK_ERR_SHAPE, "linear_noalloc: M=%d", M);
+  if (M == 0) return GQK_OK;
+  const int64_t need = gqk_linear_workspace_bytes(info, M);
+  if (need < 0) return (int)need;
+  if (need > kScratchBytes)
+    return fail(GQK_ERR_SHAPE,
+                "linear_noalloc: this plan needs %lld workspace bytes at M=%d, above the %lld-byte scratch of the "
+                "no-allocation entry point (use gqk_linear with a caller workspace)",
+                (long long)need, M, (long long)kScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return gqk_linear(packed, desc_dev, info, x, ldx, M, y, ldy, bias, need > 0 ? ws : nullptr, need > 0 ? kScratchBytes : 0,
+                    stream);
 }
 
 }  // extern "C"

@@ -19,12 +19,13 @@ GQK_ERR_ARG = -5
 GQK_FORM_GEMV = 1
 GQK_FORM_GEMM = 2
 GQK_CTR_BYTES = 262144            # the arrival-counter region at the start of every workspace
+GQK_NOALLOC_SCRATCH_BYTES = GQK_CTR_BYTES + (32 << 20)   # gqk_linear_noalloc's per-GPU device array
 GQK_DTYPE_F32, GQK_DTYPE_BF16, GQK_DTYPE_F16 = 0, 1, 2
 
 # every entry point include/gguf_hip.h declares
 EXPORTS = ("gqk_last_error", "gqk_version", "gqk_type_info", "gqk_dequantize", "gqk_dequantize_tiles",
            "gqk_tiles_bytes", "gqk_repack", "gqk_unrepack", "gqk_plan", "gqk_linear_workspace_bytes",
-           "gqk_workspace_bytes_max", "gqk_linear", "gqk_ggml_type_size",
+           "gqk_workspace_bytes_max", "gqk_linear", "gqk_linear_noalloc", "gqk_ggml_type_size",
            "gqk_gguf_open", "gqk_gguf_close", "gqk_gguf_info", "gqk_gguf_tensor_at", "gqk_gguf_find_tensor",
            "gqk_gguf_kv_at", "gqk_gguf_find_kv", "gqk_gguf_kv_string", "gqk_gguf_upload_tiles")
 
@@ -89,6 +90,7 @@ def _load() -> ctypes.CDLL:
         "gqk_linear_workspace_bytes": (i64, [ctypes.POINTER(GqkPlanInfo), i32]),
         "gqk_workspace_bytes_max": (i64, []),
         "gqk_linear": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, vp, i64, vp]),
+        "gqk_linear_noalloc": (i32, [vp, vp, ctypes.POINTER(GqkPlanInfo), vp, i64, i32, vp, i64, vp, vp]),
         "gqk_ggml_type_size": (i32, [i32, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
         "gqk_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
         "gqk_gguf_close": (None, [vp]),

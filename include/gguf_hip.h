@@ -135,6 +135,18 @@ int64_t gqk_workspace_bytes_max(void);
 int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x, int64_t ldx,
                int M, void* y, int64_t ldy, const void* bias, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* gqk_linear without a workspace argument, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart
+ * in the reference.  The split-K / stream-K counters and partials live in a file-scope device
+ * array of GQK_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends; its address is taken
+ * once per device on the first call, which also clears its counters with a fill kernel on
+ * `stream`).  Allocates nothing.  A plan that needs more workspace at this M (GEMM plans above 64
+ * rows on large layers can) is refused with GQK_ERR_SHAPE.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (other streams, other threads) race. */
+#define GQK_NOALLOC_SCRATCH_BYTES (GQK_CTR_BYTES + 33554432)
+int gqk_linear_noalloc(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x,
+                       int64_t ldx, int M, void* y, int64_t ldy, const void* bias, void* stream);
+
 /* ---- GGUF v3 files: the load path ----------------------------------------------------------
  * The reference's tensors come from vLLM's GGUF loader (gguf-py 0.17.1 GGUFReader,
  * gguf-plugin/requirements.txt:1) and are repacked at load time by _create_tiles
