@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -89,6 +90,12 @@ def cpu_baseline(seconds: float = 15.0) -> dict:
 
     cores = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(cores)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
     pool = ThreadPoolExecutor(cores)
     rng = np.random.default_rng(0)
     K, M = 5120, 8
@@ -123,7 +130,8 @@ def cpu_baseline(seconds: float = 15.0) -> dict:
     tm = statistics.median(r[1] for r in runs)
     pool.shutdown()
     return {"value": round(nbytes / (td + tm) / 1e9, 4), "unit": "GB/s", "cores": cores,
-            "kind": "port",
+            "kind": "port", "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": cpu_model,
             "sample": f"whole Q4_K + Q6_K gate_up shards (34816 x 5120 each, {nbytes} packed bytes), M={M}: "
                       f"oracle dequant {td * 1e3:.1f} ms + torch fp32 matmul {tm * 1e3:.1f} ms per pass on "
                       f"{cores} threads, median of {len(runs)} passes",
@@ -136,7 +144,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--m", type=int, default=8, help="batch rows of the decode GEMV (1..32)")
-    ap.add_argument("--copies", type=int, default=3, help="rotating weight copies (> 1 GB in total)")
+    ap.add_argument("--copies", type=int, default=3, help="rotating weight copies of the step (> 1 GB in total)")
+    ap.add_argument("--shard-bytes", type=float, default=320e6,
+                    help="per-shard timings rotate at least this many bytes of copies (> the 256 MB Infinity Cache)")
+    ap.add_argument("--stack-layers", type=int, default=64, help="config 5 lines: decoder layers (0: skip)")
     ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--detail", action="store_true", help="print the per-shard table to stderr")
@@ -172,11 +183,12 @@ def main() -> int:
         for name, N, K in SHAPES:
             if only and (gguf_hip.TYPE_NAMES[wt], name) != only:
                 continue
+            nbytes = gguf_hip.tiles_bytes(wt, N, K) // ((N + 63) // 64 * 64) * N   # packed GGUF bytes
             gls = []
-            for c in range(args.copies):
+            for c in range(max(args.copies, math.ceil(args.shard_bytes / nbytes))):
                 W = random_shard(N, K, wt, dev, seed=1000 * c + N + wt)
+                assert W.numel() == nbytes
                 gls.append(gguf_hip.pack_layer([W], [N], [wt]))
-                nbytes = W.numel()
                 del W
             shards.append((wt, name, N, K, gls, nbytes))
     torch.cuda.empty_cache()
@@ -187,7 +199,7 @@ def main() -> int:
     def step_fn(c):
         def f():
             for wt, name, N, K, gls, nb in shards:
-                gguf_hip.mul_mat_grouped(xs[K], gls[c])
+                gguf_hip.mul_mat_grouped(xs[K], gls[c % len(gls)])
         return f
 
     graphs = [_capture(step_fn(c), torch) for c in range(args.copies)]
@@ -205,19 +217,22 @@ def main() -> int:
     ms_per_step = s.elapsed_time(e) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # per-shard launch time (graph of every copy once; average per launch)
+    # per-shard launch time (graph of every copy, > 256 MB of them, twice; average per launch)
     rows = []
     for wt, name, N, K, gls, nb in shards:
-        def f(gls=gls, K=K):
-            for _ in range(4):
+        reps = max(1, 8 // len(gls))
+
+        def f(gls=gls, K=K, reps=reps):
+            for _ in range(reps):
                 for gl in gls:
                     gguf_hip.mul_mat_grouped(xs[K], gl)
         g = _capture(f, torch)
         g.replay()
-        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (4 * len(gls))
+        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (reps * len(gls))
         info = gguf_hip.ops.GqkPlanInfo.from_tuple(
             gls[0].plans[gguf_hip.ops._pick_plan(gls[0].plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
+                     "copies": len(gls),
                      "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
                      "waves_per_wg": info.nw, "one_record": info.bm == 1})
         del g
@@ -252,6 +267,26 @@ def main() -> int:
         gemm = {"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "M": Mg, "ms": round(t, 4),
                 "TFLOPs": round(tflops, 1), "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
+    stack = None
+    if args.stack_layers > 0 and not only:
+        # the mixed-type stack, the north star's "M=1..8 mixed-type GEMV"
+        from bench_configs import build_stack, time_stack
+        del shards, xs
+        torch.cuda.empty_cache()
+        grouped, _, stack_bytes, _ = build_stack(torch, gguf_hip, random_shard, dev, args.stack_layers)
+        stack = {"workload": f"BASELINE config 5: {args.stack_layers} decoder layers (seeded type draw over the eleven "
+                             "types), one mixed-type grouped launch per layer over qkv/o_proj/gate_up at K=5120 plus "
+                             "one for down", "packed_bytes": stack_bytes,
+                 "bpw": round(8 * stack_bytes / (args.stack_layers * sum(N * K for _, N, K in SHAPES)), 3),
+                 "lines": []}
+        for Ms in (1, 8):
+            t = time_stack(torch, gguf_hip, dev, grouped, Ms)
+            gbs = stack_bytes / (t * 1e-3) / 1e9
+            stack["lines"].append({"M": Ms, "ms_per_step": round(t, 4), "GBps": round(gbs, 1),
+                                   "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                                "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}})
+        del grouped
+
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True, "scaling": "weak",
@@ -266,6 +301,7 @@ def main() -> int:
                      "launch_us": dom["us"], "bytes_per_launch": dom_bytes},
         "shards": rows,
         "gemm": gemm,
+        "stack": stack,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()

@@ -118,16 +118,14 @@ def draw_stack_types(layers: int, seed: int = 5) -> list[list[int]]:
             for _ in range(layers)]
 
 
-def config5(torch, gguf_hip, random_shard, dev, ms: list[int], layers: int) -> None:
-    """BASELINE config 5: `layers` decoder layers, each with qkv / o_proj / gate_up / down of a
-    drawn type, resident in HBM (one copy: the stack itself is far beyond the Infinity Cache).
-    Two launch schedules stream the same bytes: 'grouped' = one mixed-type launch per layer over
-    its three K = 5120 matrices plus one for down (a launch needs one K), 'per_linear' = one
-    launch per matrix, as vLLM's four linear layers call it."""
+def build_stack(torch, gguf_hip, random_shard, dev, layers: int):
+    """The config-5 stack resident in HBM: per layer one mixed-type grouped layer over its three
+    K = 5120 matrices (qkv, o_proj, gate_up) and down alone ('grouped': 2 launches per layer), and
+    the same packed bytes as one layer per matrix ('per_linear': 4 launches, as vLLM's four
+    linear layers call it).  Returns (grouped, per_linear, packed GGUF bytes, types per layer)."""
     types = draw_stack_types(layers)
     grouped, per_linear = [], []
     packed_bytes = 0
-    t0 = time.perf_counter()
     for li, tl in enumerate(types):
         k5 = [(t, s) for t, s in zip(tl, LAYER_SHAPES) if s[2] == 5120]
         sizes = [gguf_hip.tiles_bytes(t, N, K) for t, (_, N, K) in k5]
@@ -154,20 +152,38 @@ def config5(torch, gguf_hip, random_shard, dev, ms: list[int], layers: int) -> N
         per_linear.append((17408, down))
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
+    return grouped, per_linear, packed_bytes, types
+
+
+def time_stack(torch, gguf_hip, dev, lst, M: int) -> float:
+    """ms per step of one pass over the stack's launches at M rows (graph replays, median)."""
+    xs = {K: torch.randn(M, K, device=dev).to(torch.bfloat16) for K in (5120, 17408)}
+
+    def f():
+        for K, gl in lst:
+            gguf_hip.mul_mat_grouped(xs[K], gl)
+    g = _capture(f, torch)
+    t = _median_ms(g, torch, 1, reps=2)
+    del g
+    return t
+
+
+def config5(torch, gguf_hip, random_shard, dev, ms: list[int], layers: int) -> None:
+    """BASELINE config 5: `layers` decoder layers, each with qkv / o_proj / gate_up / down of a
+    drawn type, resident in HBM (one copy: the stack itself is far beyond the Infinity Cache).
+    Two launch schedules stream the same bytes: 'grouped' = one mixed-type launch per layer over
+    its three K = 5120 matrices plus one for down (a launch needs one K), 'per_linear' = one
+    launch per matrix, as vLLM's four linear layers call it."""
+    t0 = time.perf_counter()
+    grouped, per_linear, packed_bytes, types = build_stack(torch, gguf_hip, random_shard, dev, layers)
     counts = {gguf_hip.TYPE_NAMES[t]: sum(tl.count(t) for tl in types) for t in ALL_TYPES}
     weights = layers * sum(N * K for _, N, K in LAYER_SHAPES)
     _emit({"config": 5, "layers": layers, "packed_bytes": packed_bytes, "weights": weights,
            "bpw": round(8 * packed_bytes / weights, 3), "type_counts": counts,
            "load_s": round(time.perf_counter() - t0, 2)})
     for M in ms:
-        xs = {K: torch.randn(M, K, device=dev).to(torch.bfloat16) for K in (5120, 17408)}
         for sched, lst in (("grouped", grouped), ("per_linear", per_linear)):
-            def f(lst=lst):
-                for K, gl in lst:
-                    gguf_hip.mul_mat_grouped(xs[K], gl)
-            g = _capture(f, torch)
-            t = _median_ms(g, torch, 1, reps=2)
-            del g
+            t = time_stack(torch, gguf_hip, dev, lst, M)
             gbs = packed_bytes / (t * 1e-3) / 1e9
             _emit({"config": 5, "schedule": sched, "M": M, "launches_per_step": len(lst), "ms_per_step": round(t, 4),
                    "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
