@@ -253,7 +253,14 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
     // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
     // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
-    const int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWaves;
+    int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWaves;
+    // Up to four rows (one token group), when every wave can hold exactly one record (k-range a
+    // multiple of four super-blocks, at most GQK_SPLIT_MAX workgroups per tile): one record per
+    // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances
+    // the CUs, which beats streaming waves there (gate_up 34816 x 5120 at M = 1: Q6_K 34.9 -> 32.5
+    // us, Q5_K 31.4 -> 28.7, IQ4_XS 30.6 -> 29.1, Q5_0 31.4 -> 28.3; the others within 1 us); at 8 rows
+    // the heavier per-record work makes the streaming plan the faster one.
+    if (target_wgs <= 0 && pi.g == 1 && nb % kGemvWaves == 0 && nb / kGemvWaves <= GQK_SPLIT_MAX) target = tiles * nb;
     const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
     const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
     const int64_t split =
