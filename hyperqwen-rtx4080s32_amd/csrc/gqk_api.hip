@@ -31,12 +31,23 @@ int check_launch(const char* what) {
   return GQK_OK;
 }
 
-// GEMV wave target when the caller gives none: eight waves per CU of a 256-CU MI355X.  A
-// workgroup takes one 64-row tile and up to four waves split its k-range (measured: more waves
-// per workgroup, or more waves than stay resident at once, run slower); shards with too few
-// tiles for the target also split K across workgroups (partials combined in-kernel).
-constexpr int kDefaultTargetWaves = 2048;
+// GEMV wave target when the caller gives none: eight waves per CU of the device current at plan
+// time (2048 on a 256-CU MI355X, also assumed when no device is visible).  A workgroup takes one
+// 64-row tile and up to four waves split its k-range (measured: more waves per workgroup, or
+// more waves than stay resident at once, run slower); shards with too few tiles for the target
+// also split K across workgroups (partials combined in-kernel).
+constexpr int kWavesPerCu = 8;
 constexpr int kGemvWaves = 4;
+
+int64_t default_target_waves() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();   // leave no error behind for the next launch check
+    cus = 256;
+  }
+  return (int64_t)kWavesPerCu * cus;
+}
 
 // bytes of the fp32 split-K partials: [tile][split][64 rows][m_max tokens]
 int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return tiles * split * 64 * m_max * 4; }
@@ -253,7 +264,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
     // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
     // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
-    int64_t target = target_wgs > 0 ? target_wgs : kDefaultTargetWaves;
+    int64_t target = target_wgs > 0 ? target_wgs : default_target_waves();
     // Up to four rows (one token group), when every wave can hold exactly one record (k-range a
     // multiple of four super-blocks, at most GQK_SPLIT_MAX workgroups per tile): one record per
     // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances

@@ -75,6 +75,15 @@ def _require_gpu(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what}: the tensor must be on a GPU (there is no CPU path), got {t.device}")
 
 
+def _addr_aligned(t: torch.Tensor, align: int) -> bool:
+    """t's first element at an address that is a multiple of align.  Under tracing (FakeTensor,
+    torch.compile) a tensor has no address: its byte offset into the storage decides, storages
+    being allocated at least 256-byte aligned."""
+    if torch.compiler.is_compiling() or isinstance(t, torch._subclasses.fake_tensor.FakeTensor):
+        return t.storage_offset() * t.element_size() % align == 0
+    return t.data_ptr() % align == 0
+
+
 def _rows_view(W: torch.Tensor, what: str) -> torch.Tensor:
     if W.dtype != torch.uint8 or W.dim() != 2:
         raise ValueError(f"{what}: expected uint8 [rows, bytes], got {W.dtype} {tuple(W.shape)}")
@@ -334,7 +343,7 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
     if x.dim() != 2 or x.shape[1] != gl.K:
         raise ValueError(f"mul_mat_grouped: x {tuple(x.shape)} does not match K={gl.K}")
     xb = x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)
-    if xb.stride(1) != 1 or xb.stride(0) % 8 or xb.data_ptr() % 16:
+    if xb.stride(1) != 1 or xb.stride(0) % 8 or not _addr_aligned(xb, 16):
         xb = xb.contiguous()
     ws = gl.workspace if workspace is None else workspace
     fused = None

@@ -103,8 +103,9 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
 /* Host-only: the launch plan of a grouped layer (shards packed back to back, all of K columns)
  * for batch rows M: fills *info and, if desc is not NULL and desc_capacity (int32 words) is
  * enough, the descriptor table (16 int32 per row) to upload to the device.  target_wgs > 0
- * overrides the GEMV heuristic's target of resident waves (0 = default), from which the waves
- * per workgroup and the split-K factor follow.  Replaces
+ * overrides the GEMV heuristic's target of resident waves (0 = default: eight per CU of the
+ * device current at the call, 256 CUs assumed when none is visible), from which the waves per
+ * workgroup and the split-K factor follow.  Replaces
  * prepare_grouped_layer / descriptors / grouped_split_for
  * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
 int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
