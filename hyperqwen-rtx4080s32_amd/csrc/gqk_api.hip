@@ -270,8 +270,14 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances
     // the CUs, which beats streaming waves there (gate_up 34816 x 5120 at M = 1: Q6_K 34.9 -> 32.5
     // us, Q5_K 31.4 -> 28.7, IQ4_XS 30.6 -> 29.1, Q5_0 31.4 -> 28.3; the others within 1 us); at 8 rows
-    // the heavier per-record work makes the streaming plan the faster one.
-    if (target_wgs <= 0 && pi.g == 1 && nb % kGemvWaves == 0 && nb / kGemvWaves <= GQK_SPLIT_MAX) target = tiles * nb;
+    // the heavier per-record work makes the streaming plan the faster one for a single type.  A
+    // mixed-type layer takes it up to eight rows: its streaming kernel holds the registers of its
+    // costliest format (~235 VGPRs: two waves per SIMD) where the one-record kernel needs ~100
+    // (a mixed stack's qkv + o_proj + gate_up launches at K = 5120, M = 8: 49.0 -> 43.2 us per layer; at 16
+    // rows no gain, and splitting `down`'s 68 super-blocks 17 ways measured no better either).
+    if (target_wgs <= 0 && (pi.g == 1 || (mixed && pi.g == 2)) && nb % kGemvWaves == 0 &&
+        nb / kGemvWaves <= GQK_SPLIT_MAX)
+      target = tiles * nb;
     const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
     const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
     const int64_t split =

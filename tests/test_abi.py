@@ -144,17 +144,27 @@ def test_plan_gemv_tail_tiles_split():
     info, desc = ops.plan([(12, 64 * 800, 0)], 5120, 8, 0)
     ncs = _check_gemv_rows([(12, 64 * 800, 0)], 5120, info, desc)
     assert info.nw == 3 and sorted(ncs.values()) == [1] * 682 + [2] * 118
-    # the tail spans shards: Q6_K 34816 rows after a 1024-row Q4_K shard (560 tiles, 48 split)
-    off = ops.tiles_bytes(12, 1024, 5120)
-    info, desc = ops.plan([(12, 1024, 0), (14, 34816, off)], 5120, 8, 0)
-    ncs = _check_gemv_rows([(12, 1024, 0), (14, 34816, off)], 5120, info, desc)
+    # the tail spans shards: 34816 rows after a 1024-row shard of the same type (560 tiles, 48 split)
+    offq = ops.tiles_bytes(14, 1024, 5120)
+    info, desc = ops.plan([(14, 1024, 0), (14, 34816, offq)], 5120, 8, 0)
+    ncs = _check_gemv_rows([(14, 1024, 0), (14, 34816, offq)], 5120, info, desc)
     assert sum(1 for v in ncs.values() if v > 1) == 48 and info.split == min(5, 256 // 48)
+    off = ops.tiles_bytes(12, 1024, 5120)
     # up to four rows the same layer takes one record per wave: every tile split 5 ways x 4 waves
     info, desc = ops.plan([(12, 1024, 0), (14, 34816, off)], 5120, 1, 0)
     ncs = _check_gemv_rows([(12, 1024, 0), (14, 34816, off)], 5120, info, desc)
     assert set(ncs.values()) == {5} and info.n_desc == 560 * 5 and info.nw == 4 and info.bm == 1
     # ... unless the k-range does not split into single records (down: 68 super-blocks)
     assert ops.plan([(12, 5120, 0)], 17408, 1, 0)[0].bm == 0
+    # a mixed-type layer keeps one record per wave up to eight rows (its streaming kernel is bound
+    # by its costliest format's registers); a single type streams at eight, and nothing does at 16
+    mixed = [(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))]
+    for M, bm in ((1, 1), (8, 1), (16, 0)):
+        info, desc = ops.plan(mixed, 5120, M, 0)
+        assert info.bm == bm and info.types_mask == 0, M
+        if bm:
+            assert set(_check_gemv_rows(mixed, 5120, info, desc).values()) == {5} and info.n_desc == 192 * 5
+    assert ops.plan([(12, 7168, 0)], 5120, 8, 0)[0].bm == 1 and ops.plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
     # one round of split tiles with >= 2 records a wave fills the 512 slots exactly: down 5120 x
     # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; qkv (1 record a wave) keeps 5 each
     info, desc = ops.plan([(12, 5120, 0)], 17408, 8, 0)
