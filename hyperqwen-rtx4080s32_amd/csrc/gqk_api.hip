@@ -244,14 +244,10 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
                 (long long)tiles, (long long)(64 * tiles), GQK_CTR_WORDS);
   const int64_t ctr_bytes = GQK_CTR_BYTES;
   pi.ctr_bytes = (int32_t)ctr_bytes;
-  // The GEMV serves up to 16 rows; layers with a table type (IQ4_NL / IQ4_XS / IQ3_S, whose
-  // lookups cost the GEMV the most per weight) switch to the 32-row GEMM above 8 rows, which
-  // measured faster there (IQ4_XS 34816 x 5120 at M = 16: 64 us GEMV, ~50 us GEMM).
-  bool table_type = false;
-  for (int i = 0; i < nshards; ++i)
-    table_type |= shards[i].ggml_type == GQK_IQ4_NL || shards[i].ggml_type == GQK_IQ4_XS || shards[i].ggml_type == GQK_IQ3_S;
-  const int gemv_max = table_type ? 8 : GQK_GEMV_MAX_M;
-  if (M <= gemv_max) {
+  // The GEMV serves up to 16 rows for every type (with its x operands broadcast from registers
+  // the table types too beat the 32-row GEMM at 16 rows: IQ4_NL / IQ3_S / IQ4_XS 34816 x 5120
+  // 41 / 43 / 42 us against 51 / 56 / 50 us, 5120 x 17408 26-28 us against 39-46 us).
+  if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
 #ifdef GQK_GEMV_MIN_G

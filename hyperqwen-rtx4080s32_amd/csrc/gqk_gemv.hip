@@ -339,6 +339,29 @@ __device__ __forceinline__ void slots_of_group(const uint4 (&v)[4], uint2 (&o)[8
   }
 }
 
+// The 4 x 4 x 4 (16 blocks) MFMA with block ab's A operand broadcast to every block (CBSZ = 4,
+// ABID = ab), and the 4 x 4 x 1 fp32 one likewise.  ab must fold to a constant (unrolled loops).
+#define GQK_AB_CASES(F) F(0) F(1) F(2) F(3) F(4) F(5) F(6) F(7) F(8) F(9) F(10) F(11) F(12) F(13) F(14) F(15)
+__device__ __forceinline__ v4f mfma4_bcast(int ab, v4s a, v4s b, v4f c) {
+  switch (ab) {
+#define GQK_CASE(k) case k: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 4, k, 0);
+    GQK_AB_CASES(GQK_CASE)
+#undef GQK_CASE
+  }
+  return c;
+}
+__device__ __forceinline__ v4f mfma1_bcast(int ab, float a, float b, v4f c) {
+  switch (ab) {
+#define GQK_CASE(k) case k: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 4, k, 0);
+    GQK_AB_CASES(GQK_CASE)
+#undef GQK_CASE
+  }
+  return c;
+}
+
+template <int G, int T>
+constexpr bool x_broadcast() { return !(G == 2 && T == GQK_Q6_K); }
+
 template <int MPAD>
 struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16 + 8 group sums x MPAD
   static constexpr int X = 64 * MPAD * 8;
@@ -437,8 +460,22 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
   const float* xsum32 = xsum16 + 16 * MPAD;
   if (kw0 >= kw1) return;
 
+  // The x operands come from registers, 16 slots per register pair: lane 4b + i holds token
+  // 4g + i's x at slot 16j + b, and each MFMA broadcasts block (slot % 16)'s operand to all 16
+  // blocks (CBSZ = 4, ABID = slot % 16), so a wave reads each slot's x from LDS once instead of
+  // once per MFMA.  The group sums likewise: lane 4b + i holds token 4g + i's sum of group b.
+  // (Q6_K at G = 2 keeps one LDS read per MFMA: with the operand registers its kernel spills at
+  // the three-waves bound, and measured 5% slower.)
+  constexpr bool XB = x_broadcast<G, T>();
+  const int bl = lane >> 2;
   // one record (super-block) of the lane's row: MFMA chains per scale group, fp32 epilogue
   auto process = [&](const D& rec) {
+    const float* xsm = (D::SUB == 16 ? xsum16 : xsum32) + (XB ? min(bl, NSUB - 1) * MPAD : 0);
+    float xq[G];
+    if constexpr (XB)
+#pragma unroll
+      for (int g = 0; g < G; ++g) xq[g] = xsm[4 * g + li];
+    uint2 xa[G];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
       float scale, bias;
@@ -452,18 +489,26 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
         rec.pair(s, m, b0, b1, tb, mk);
         v4s B = __builtin_bit_cast(v4s, make_uint2(b0, b1));
         const int slot = s * MPS + m;
+        if constexpr (XB) {
+          if (slot % 16 == 0)
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          v4s A = __builtin_bit_cast(v4s, xs[x_slot<MPAD, x_groups_adjacent<T>()>(slot, 4 * g + li)]);
-          C[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A, B, C[g], 0, 0, 0);
+            for (int g = 0; g < G; ++g) xa[g] = xs[x_slot<MPAD, x_groups_adjacent<T>()>(slot + bl, 4 * g + li)];
+#pragma unroll
+          for (int g = 0; g < G; ++g) C[g] = mfma4_bcast(slot % 16, __builtin_bit_cast(v4s, xa[g]), B, C[g]);
+        } else {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            v4s A = __builtin_bit_cast(v4s, xs[x_slot<MPAD, x_groups_adjacent<T>()>(slot, 4 * g + li)]);
+            C[g] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(A, B, C[g], 0, 0, 0);
+          }
         }
       }
-      const float* xsm = (D::SUB == 16 ? xsum16 + s * MPAD : xsum32 + s * MPAD);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         if constexpr (BIAS) {
           // acc[i][row] -= sum_x[token i] * bias[row]: an fp32 outer product per 4x4 block
-          acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(xsm[4 * g + li], -bias, acc[g], 0, 0, 0);
+          if constexpr (XB) acc[g] = mfma1_bcast(s, xq[g], -bias, acc[g]);
+          else acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(xsm[s * MPAD + 4 * g + li], -bias, acc[g], 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[g][i] = __builtin_fmaf(scale, C[g][i], acc[g][i]);

@@ -285,13 +285,12 @@ def test_plan_buckets():
     assert ops._pick_plan([], 17) == 3 and ops._pick_plan([], 32) == 3 and ops._pick_plan([], 33) == 4
     assert ops._pick_plan([], 64) == 4 and ops._pick_plan([], 65) == 5 and ops._pick_plan([], 128) == 5
     assert ops._pick_plan([], 129) == 6 and ops._pick_plan([], 8192) == 6
-    # a layer with a table type (IQ4_NL / IQ4_XS / IQ3_S) leaves the GEMV above 8 rows
+    # every type, the table types (IQ4_NL / IQ4_XS / IQ3_S) included, stays on the GEMV up to 16 rows
     for wt in (20, 23, 21):
-        assert ops.plan([(wt, 512, 0)], 512, 8)[0].form == 1
-        i9, i16 = ops.plan([(wt, 512, 0)], 512, 9)[0], ops.plan([(wt, 512, 0)], 512, 16)[0]
-        assert (i9.form, i9.bm, i16.form, i16.bm) == (2, 32, 2, 32)
+        i9, i16, i17 = (ops.plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17))
+        assert (i9.form, i9.g, i16.form, i16.g, i17.form, i17.bm) == (1, 4, 1, 4, 2, 32)
     off = ops.tiles_bytes(12, 512, 512)
-    assert ops.plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 2
+    assert ops.plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 1
     for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 256), (2048, 256)):
         assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm
 
