@@ -359,8 +359,14 @@ __device__ __forceinline__ v4f mfma1_bcast(int ab, float a, float b, v4f c) {
   return c;
 }
 
-template <int G, int T>
-constexpr bool x_broadcast() { return !(G == 2 && T == GQK_Q6_K); }
+// Which x operands a kernel broadcasts from registers (the MFMA operands, the group sums).  Q6_K
+// at G = 2 sits at the three-waves register bound: its streaming kernel broadcasts the operands
+// but reads the sums from LDS (with both it spills; as chosen, down / gate_up 4% / 1-2% faster
+// than neither), and its one-record kernel keeps both in LDS (0.2 us faster on qkv than either).
+template <int G, int T, bool ONE>
+constexpr bool x_broadcast() { return !(G == 2 && T == GQK_Q6_K && ONE); }
+template <int G, int T, bool ONE>
+constexpr bool xq_broadcast() { return !(G == 2 && T == GQK_Q6_K); }
 
 template <int MPAD>
 struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16 + 8 group sums x MPAD
@@ -464,15 +470,13 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
   // 4g + i's x at slot 16j + b, and each MFMA broadcasts block (slot % 16)'s operand to all 16
   // blocks (CBSZ = 4, ABID = slot % 16), so a wave reads each slot's x from LDS once instead of
   // once per MFMA.  The group sums likewise: lane 4b + i holds token 4g + i's sum of group b.
-  // (Q6_K at G = 2 keeps one LDS read per MFMA: with the operand registers its kernel spills at
-  // the three-waves bound, and measured 5% slower.)
-  constexpr bool XB = x_broadcast<G, T>();
+  constexpr bool XB = x_broadcast<G, T, ONE>(), XQ = xq_broadcast<G, T, ONE>();
   const int bl = lane >> 2;
   // one record (super-block) of the lane's row: MFMA chains per scale group, fp32 epilogue
   auto process = [&](const D& rec) {
-    const float* xsm = (D::SUB == 16 ? xsum16 : xsum32) + (XB ? min(bl, NSUB - 1) * MPAD : 0);
+    const float* xsm = (D::SUB == 16 ? xsum16 : xsum32) + (XQ ? min(bl, NSUB - 1) * MPAD : 0);
     float xq[G];
-    if constexpr (XB)
+    if constexpr (XQ)
 #pragma unroll
       for (int g = 0; g < G; ++g) xq[g] = xsm[4 * g + li];
     uint2 xa[G];
@@ -507,7 +511,7 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
       for (int g = 0; g < G; ++g) {
         if constexpr (BIAS) {
           // acc[i][row] -= sum_x[token i] * bias[row]: an fp32 outer product per 4x4 block
-          if constexpr (XB) acc[g] = mfma1_bcast(s, xq[g], -bias, acc[g]);
+          if constexpr (XQ) acc[g] = mfma1_bcast(s, xq[g], -bias, acc[g]);
           else acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(xsm[s * MPAD + 4 * g + li], -bias, acc[g], 0, 0, 0);
         }
 #pragma unroll
