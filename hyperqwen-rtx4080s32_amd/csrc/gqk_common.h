@@ -130,7 +130,7 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 #define GQK_CTR_BYTES 262144   // (mirrored in include/gguf_hip.h)
 #define GQK_CTR_WORDS (GQK_CTR_BYTES / 4)
 #ifndef GQK_GEMV_MAX_M
-#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form (8 for layers with an IQ type); the GEMM above
+#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form (every type); the GEMM above
 #endif
 #define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
 enum {

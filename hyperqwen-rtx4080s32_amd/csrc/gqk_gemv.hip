@@ -374,8 +374,9 @@ struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16
   static constexpr int BYTES = X + 24 * MPAD * 4;
 };
 
-// Order of the x slots in LDS.  An MFMA of token group g reads, in lane 4b + i, the 8 bytes of
-// token 4g + i at its slot.  Groups adjacent ([slot][i][g]): the G groups' operands of a lane are
+// Order of the x slots in LDS.  Lane 4b + i reads the 8 bytes of token 4g + i at a slot (once per
+// 16 slots with the broadcast operands, once per MFMA without).  The orders were chosen when every
+// MFMA read its operand from LDS; measured then:  Groups adjacent ([slot][i][g]): the G groups' operands of a lane are
 // one 8 G-byte run, a single ds_read_b128 at G = 2 (M = 8: IQ types 7-9% faster, Q4_K 3%, Q5_K 2%;
 // M = 16: up to 5%).  Tokens in order ([slot][t]): two 8-byte reads 32 bytes apart (ds_read2_b64);
 // kept for Q8_0 and Q5_0, whose one-record kernels measured 4-8% slower with the adjacent order
