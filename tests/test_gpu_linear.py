@@ -260,6 +260,36 @@ def test_mixed_layer_one_launch(dev):
             col += n
 
 
+def test_mixed_layer_default_plan_one_record(dev):
+    """All eleven types in one mixed launch at the default plan: up to eight rows one record per
+    wave (the mixed one-record kernels, K split five ways through the in-kernel exchange), at 16
+    rows the G = 4 kernel; it matches the oracle, repeats bit-identically and leaves the counters
+    at zero.  (For 22 tiles the streaming heuristic lands on the one-record plan by itself; the
+    config-5 layers exercise the mixed-layer rule at 736 tiles.)"""
+    import gguf_hip
+
+    rng = np.random.default_rng(71)
+    K = 20 * 256
+    shards = [(wt, 64 * (1 + i % 3) - 7 * (i % 2)) for i, wt in enumerate(G.ALL_TYPES)]
+    raws = [G.random_blocks(rng, n, K, wt) for wt, n in shards]
+    wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
+    gl = gguf_hip.pack_layer([torch.from_numpy(r).to(dev) for r in raws], [n for _, n in shards],
+                             [wt for wt, _ in shards])
+    for M in (1, 5, 8, 16):
+        i = gguf_hip.ops._pick_plan(gl.plans, M)
+        info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[i * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
+        assert info.form == 1 and info.types_mask == 0, M
+        if M <= 8:
+            assert info.bm == 1 and info.split == 5 and info.nw == 4, M
+        x = _x(M, K, 7100 + M, dev)
+        y = gguf_hip.mul_mat_grouped(x, gl)
+        assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
+        for _ in range(3):
+            assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y), M
+    torch.cuda.synchronize()
+    assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
+
+
 class _WT:
     def __init__(self, weight_type, shard_weight_type=None):
         self.weight_type = weight_type
