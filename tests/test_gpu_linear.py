@@ -31,7 +31,7 @@ def test_gemv_and_gemm_all_types(dev, wt):
     wf = G.dequantize(raw, wt)
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt])
     worst = 0.0
-    for M in (1, 2, 3, 4, 5, 8, 9, 16, 17, 32, 33, 64, 65, 130):
+    for M in (1, 2, 3, 4, 5, 6, 8, 9, 12, 13, 16, 17, 32, 33, 64, 65, 130):
         x = _x(M, K, 1000 + M, dev)
         y = gguf_hip.mul_mat_grouped(x, gl)
         torch.cuda.synchronize()
