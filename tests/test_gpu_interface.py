@@ -79,6 +79,29 @@ def test_gluon_mul_mat_strided_shards_in_graph(dev):
         I.gluon_mul_mat(_x(1, K, 0, dev), views[0], 16, 130)          # IQ2_XXS: no kernel here
 
 
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_gluon_mul_mat_every_type_strided(dev, wt):
+    """gluon_mul_mat on a shard view with a row stride wider than its rows and a column offset
+    (the plugin's weight[start:end, :size], gguf-plugin/gluon/interface.py:74-80), every type, at
+    GEMV and GEMM row counts: oracle within 1e-2, one cache entry on the base, repeat bit-identity."""
+    from gguf_hip import interface as I
+
+    rng = np.random.default_rng(900 + wt)
+    n, K = 150, 1024
+    raw = G.random_blocks(rng, n, K, wt)
+    big = np.zeros((n + 30, raw.shape[1] + 48), np.uint8)
+    big[10:10 + n, 32:32 + raw.shape[1]] = raw
+    W = torch.from_numpy(big).to(dev)
+    view = W[10:10 + n, 32:32 + raw.shape[1]]
+    wf = G.dequantize(raw, wt)
+    for M in (1, 7, 16, 40):
+        x = _x(M, K, 950 + M, dev)
+        y = I.gluon_mul_mat(x, view, wt, n)
+        assert y.shape == (M, n) and G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, (G.NAMES[wt], M)
+        assert torch.equal(I.gluon_mul_mat(x, view, wt, n), y), (G.NAMES[wt], M)
+    assert len(W._gguf_hip_layers) == 1
+
+
 def test_prepare_and_grouped_call_like_the_plugin(dev):
     """prepare_grouped_layer / gluon_mul_mat_tiles_grouped with the reference's argument tuple
     (gguf-plugin/patches/gguf-tiles-grouped.patch:106-115,130-136), and the tile views'
