@@ -19,9 +19,11 @@
 // tokens x 4 k).  One chain of MFMAs covers one scale group (16 or 32 weights); the epilogue
 // applies it in fp32:  y += (d * sc) * C - (c * d * sc + dmin * m) * sum(x over the group), the
 // second term as one v_mfma_f32_4x4x1f32 outer product (token sums x row biases) per group.
-// The group sums of x are computed once per workgroup when x is staged into LDS.  Products
-// bf16 x exact-integer are exact in the MFMA, accumulation is fp32, so the result equals an
-// fp32 matmul of the gguf-py weights up to summation order.
+// The x operands (A) and the group sums of x are computed once per record when the wave stages
+// its x slice into LDS; the MFMAs then take them from registers through the block broadcast
+// (CBSZ / ABID), one LDS read per 16 slots.  Products bf16 x exact-integer are exact in the
+// MFMA, accumulation is fp32, so the result equals an fp32 matmul of the gguf-py weights up to
+// summation order.
 //
 // Split-K: a tile shared by several workgroups (k-ranges) gets fp32 partial slots
 // [slot][row][token]; the last workgroup of the tile to arrive sums them in split order
