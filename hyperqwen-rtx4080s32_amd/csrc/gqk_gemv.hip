@@ -67,13 +67,16 @@ __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, int b) { return (
 // v_and_or_b32.  The values are hidden from constant folding by empty asm statements (no
 // instruction is emitted), so the compiler still schedules the ALU ops and their MFMA hazards.
 struct Masks {
-  uint32_t f, ff, t3, mg, m43;   // 0x000F000F, 0x00FF00FF, 0x00030003 (SGPRs); 0x43004300, 0x43434343 (VGPRs)
+  // 0x000F000F, 0x00FF00FF, 0x00030003, 0x000C000C, 0x00300030 (SGPRs); 0x43004300, 0x43434343 (VGPRs)
+  uint32_t f, ff, t3, t3b, t3c, mg, m43;
 };
 __device__ __forceinline__ Masks make_masks() {
-  Masks k{0x000F000Fu, 0x00FF00FFu, 0x00030003u, 0x43004300u, 0x43434343u};
+  Masks k{0x000F000Fu, 0x00FF00FFu, 0x00030003u, 0x000C000Cu, 0x00300030u, 0x43004300u, 0x43434343u};
   asm volatile("" : "+s"(k.f));
   asm volatile("" : "+s"(k.ff));
   asm volatile("" : "+s"(k.t3));
+  asm volatile("" : "+s"(k.t3b));
+  asm volatile("" : "+s"(k.t3c));
   asm volatile("" : "+v"(k.mg));
   asm volatile("" : "+v"(k.m43));
   return k;
@@ -146,6 +149,14 @@ template <> struct Dec<GQK_Q8_0> {
   }
 };
 
+// Q2_K / Q3_K: the 2-bit field of scale group s sits at bits 2t .. 2t + 1 of each byte (t =
+// (s >> 1) & 3).  It is masked where it sits rather than shifted down: the bf16 pattern
+// 0x4300 | (u << p) is exactly 128 + 2^p u while bit p + 2 (Q3_K: p + 3) stays below the
+// exponent, and the group's scale is divided by 2^p (exact).  p = 2t for t <= 2; the t = 3 field
+// is shifted down to p = 2 (Q2_K) or p = 4 (Q3_K, whose third bit needs room above it).
+__device__ constexpr float q2_inv(int t) { return t == 0 ? 1.f : t == 2 ? 0.0625f : 0.25f; }
+__device__ constexpr float q3_inv(int t) { return t == 0 ? 1.f : t == 1 ? 0.25f : 0.0625f; }
+
 template <> struct Dec<GQK_Q2_K> {
   static constexpr int SUB = 16, FAM = FAM_SWAP, REC = 84;
   uint32_t qs[16], sc[4], dd;
@@ -154,15 +165,17 @@ template <> struct Dec<GQK_Q2_K> {
   }
   __device__ void scales(int s, float& scale, float& b) const {
     uint32_t sb = byte_of(sc, s);
-    float d = h2f(dd), dmin = h2f(dd >> 16);
-    scale = d * (float)(sb & 0xF);
+    const float d = h2f(dd), dmin = h2f(dd >> 16);
+    scale = (d * q2_inv((s >> 1) & 3)) * (float)(sb & 0xF);   // d 2^-p: one product per p (exact)
     b = 128.f * scale + dmin * (float)(sb >> 4);
   }
   __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int h = s >> 3, t = (s >> 1) & 3, hf = s & 1;
-    uint32_t w = qs[8 * h + 4 * hf + m] >> (2 * t);
-    b0 = and_or(w, k.t3, k.mg);
-    b1 = and_or(w >> 8, k.t3, k.mg);
+    const uint32_t w = qs[8 * h + 4 * hf + m];
+    const uint32_t v = t == 3 ? w >> 4 : w;
+    const uint32_t msk = t == 0 ? k.t3 : t == 2 ? k.t3c : k.t3b;
+    b0 = and_or(v, msk, k.mg);
+    b1 = and_or(v >> 8, msk, k.mg);
   }
 };
 
@@ -179,14 +192,19 @@ template <> struct Dec<GQK_Q3_K> {
   __device__ void scales(int s, float& scale, float& b) const {
     int lo = (byte_of(sb, s % 8) >> (4 * (s / 8))) & 0xF;
     int hi = (byte_of(sb, 8 + s % 4) >> (2 * (s / 4))) & 3;
-    scale = h2f(d16) * (float)((lo | (hi << 4)) - 32);
-    b = 132.f * scale;
+    const float inv = q3_inv((s >> 1) & 3);
+    scale = (h2f(d16) * inv) * (float)((lo | (hi << 4)) - 32);   // d 2^-p: one product per p (exact)
+    b = (128.f + 4.f / inv) * scale;                              // 128 2^-p d sc + 4 d sc, exact
   }
   __device__ void pair(int s, int m, uint32_t& b0, uint32_t& b1, const Tabs&, const Masks& k) const {
     int n = s >> 3, j = (s >> 1) & 3, hf = s & 1;
-    uint32_t q = (qs[8 * n + 4 * hf + m] >> (2 * j)) & 0x03030303u;
-    uint32_t h = (hm[4 * hf + m] >> (4 * n + j)) & 0x01010101u;
-    uint32_t u = q | (h << 2);
+    const int p = j == 3 ? 4 : 2 * j;                        // where the 3-bit value lands
+    const uint32_t qd = qs[8 * n + 4 * hf + m];
+    const uint32_t q = (j == 3 ? qd >> 2 : qd) & (0x03030303u << p);
+    const int hs = 4 * n + j - (p + 2);                      // the hmask bit (4n + j) -> bit p + 2
+    const uint32_t hd = hm[4 * hf + m];
+    const uint32_t h = hs >= 0 ? hd >> hs : hd << -hs;
+    const uint32_t u = and_or(h, 0x04040404u << p, q);
     split_bytes(u, k, b0, b1);
   }
 };
