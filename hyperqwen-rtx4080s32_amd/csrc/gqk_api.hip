@@ -348,6 +348,37 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     pi.workspace_bytes = 0;
   }
   pi.n_desc = (int32_t)(rows.size() / GQK_DESC_WORDS);
+  bool all_split = pi.form == GQK_FORM_GEMV;
+  for (int64_t r = 0; all_split && r < pi.n_desc; ++r) all_split = rows[r * GQK_DESC_WORDS + D_NC] > 1;
+  if (all_split) {
+    // A plan whose tiles are all split (one record per wave; `down`): workgroup i runs on XCD
+    // i % 8 (the dispatcher deals workgroups to the XCDs in turn), so the tiles go eight at a time
+    // with their splits interleaved (workgroup 8 s + x = split s of the group's tile x): all
+    // contributors of a tile share one XCD and its L2 for the exchange, and every XCD gets the
+    // same work (qkv / o_proj 1.5-3.4% faster).  Plans with whole tiles keep their order (putting
+    // their split tail first measured up to 6% slower).
+    const int64_t n = pi.n_desc;
+    std::vector<int32_t> out;
+    out.reserve(rows.size());
+    auto row_at = [&](int64_t r) { return rows.begin() + r * GQK_DESC_WORDS; };
+    std::vector<std::pair<int64_t, int>> tiles_split;   // (first row, contributors)
+    for (int64_t r = 0; r < n;) {
+      const int nc = row_at(r)[D_NC];
+      if (nc > 1) tiles_split.push_back({r, nc});
+      r += nc;
+    }
+    for (size_t a = 0; a < tiles_split.size();) {
+      size_t b = a;
+      while (b < tiles_split.size() && b - a < 8 && tiles_split[b].second == tiles_split[a].second) ++b;
+      for (int sidx = 0; sidx < tiles_split[a].second; ++sidx)
+        for (size_t t = a; t < b; ++t) {
+          auto it = row_at(tiles_split[t].first + sidx);
+          out.insert(out.end(), it, it + GQK_DESC_WORDS);
+        }
+      a = b;
+    }
+    rows.swap(out);
+  }
   *info = pi;
   if (desc) {
     if (desc_capacity < (int64_t)rows.size())

@@ -182,6 +182,30 @@ def test_plan_gemv_tail_tiles_split():
     assert info.nw == 2 and sorted(ncs.values()) == [1] * 8 + [2, 2]
 
 
+def test_plan_all_split_rows_interleaved_by_xcd():
+    """A GEMV plan whose tiles are all split deals them eight at a time with their splits
+    interleaved, so every contributor of a tile sits at workgroup indices of one residue mod 8
+    (the dispatcher deals workgroups to the eight XCDs in turn) and the residues get equal work;
+    a plan with whole tiles keeps the tile order."""
+    from gguf_hip import ops
+
+    for shards, K, M in (([(12, 5120, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 7168, 0)], 5120, 1),
+                         ([(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))], 5120, 8)):
+        info, desc = ops.plan(shards, K, M)
+        d = _rows(desc)
+        assert all(r[12] > 1 for r in d), (shards, K, M)
+        _check_gemv_rows([(wt, n, o) for wt, n, o in shards], K, info, desc)
+        residues, work = {}, [0] * 8
+        for i, r in enumerate(d):
+            residues.setdefault((int(r[1]) | int(r[2]) << 32, int(r[3])), set()).add(i % 8)
+            work[i % 8] += int(r[6]) - int(r[5])
+        assert all(len(v) == 1 for v in residues.values()), (shards, K, M)
+        assert max(work) - min(work) <= K // 256, (shards, K, M, work)
+    info, desc = ops.plan([(12, 34816, 0)], 5120, 8)            # 512 whole tiles + a split tail
+    tiles = [int(r[3]) for r in _rows(desc)]
+    assert tiles[:512] == list(range(512)) and tiles == sorted(tiles)
+
+
 def test_plan_random_layers_stay_in_bounds():
     """Seeded random layers (1-4 shards of random types and row counts, K up to 80 super-blocks,
     M 1-600, default / tiny / odd wave targets): every descriptor row addresses a tile of its own
