@@ -354,7 +354,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // A plan whose tiles are all split (one record per wave; `down`): workgroup i runs on XCD
     // i % 8 (the dispatcher deals workgroups to the XCDs in turn), so the tiles go eight at a time
     // with their splits interleaved (workgroup 8 s + x = split s of the group's tile x): all
-    // contributors of a tile share one XCD and its L2 for the exchange, and every XCD gets the
+    // contributors of a tile share one XCD (for the exchange's round trips), and every XCD gets the
     // same work (qkv / o_proj 1.5-3.4% faster).  Plans with whole tiles keep their order (putting
     // their split tail first measured up to 6% slower).
     const int64_t n = pi.n_desc;
