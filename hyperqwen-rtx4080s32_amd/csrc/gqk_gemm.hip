@@ -397,6 +397,16 @@ typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;    // M > 128: 8 waves, one workgroup 
 typedef Geo<128, 128, 2, 2, 1, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
 typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 33..64 tokens
 typedef Geo<32, 128, 1, 4, 1, 2> GeoTiny;    // 17..32 tokens: 4 waves side by side, three workgroups per CU
+// The 256 x 256 tile with its 8 waves 2 x 4 (128 tokens x 64 rows each) instead of 4 x 2: the
+// same fragment reads per step, another LDS access and register schedule.  Measured on both
+// 34816 x 5120 and 5120 x 17408 shards at M = 512 / 2048 / 8192, it is 2-7% faster for Q5_0,
+// Q5_K, Q6_K and IQ4_XS and 1-5% slower for Q4_0, Q8_0, Q3_K, Q4_K, IQ4_NL and IQ3_S (Q2_K
+// even), so each type takes the faster grid.  A 8 x 1 grid was slower for every type tried.
+typedef Geo<256, 256, 2, 4, 2, 2> GeoBigWide;
+template <class GE, int T> struct geo_of { typedef GE type; };
+template <int T> struct geo_of<GeoBig, T> {
+  typedef std::conditional_t<T == GQK_Q5_0 || T == GQK_Q5_K || T == GQK_Q6_K || T == GQK_IQ4_XS, GeoBigWide, GeoBig> type;
+};
 
 template <int S, class V>
 __device__ __forceinline__ V& pick(V& a, V& b, V& c) {
@@ -833,7 +843,7 @@ static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const 
   const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb);
   dim3 grid((unsigned)(T >= G ? G : gsk));
   switch (only) {
-#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<GE, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, bias, part, ctr, G, gsk); return GQK_OK;
+#define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<typename geo_of<GE, T>::type, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, bias, part, ctr, G, gsk); return GQK_OK;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
     C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
 #undef C

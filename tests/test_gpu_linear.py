@@ -31,7 +31,7 @@ def test_gemv_and_gemm_all_types(dev, wt):
     wf = G.dequantize(raw, wt)
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt])
     worst = 0.0
-    for M in (1, 2, 3, 4, 5, 6, 8, 9, 12, 13, 16, 17, 32, 33, 64, 65, 130):
+    for M in (1, 2, 3, 4, 5, 6, 8, 9, 12, 13, 16, 17, 32, 33, 64, 65, 130, 300):
         x = _x(M, K, 1000 + M, dev)
         y = gguf_hip.mul_mat_grouped(x, gl)
         torch.cuda.synchronize()
@@ -446,20 +446,22 @@ def test_baseline_config1_q8_0(dev):
                                    (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120),
                                    (1000, 2048, 20), (5120, 5120, 32), (200000, 256, 30)],
                          ids=str)
-def test_gemm_stream_k_schedule(dev, n, K, M):
+@pytest.mark.parametrize("wt", [G.Q5_K, G.Q4_K], ids=lambda t: G.NAMES[t])
+def test_gemm_stream_k_schedule(dev, n, K, M, wt):
     """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows; 128 x 128, 64 x 128 and
     32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
     tiles' k-steps split over up to all of them (stream-K, >= 16 steps each, <= 6 per tile) and
     combined in k order by the last contributor.  Small grids are all remainder; the 16384-row
-    case at M=1100 and the 70000- and 200000-row cases mix both phases.  Checked
+    case at M=1100 and the 70000- and 200000-row cases mix both phases.  Q5_K runs the 256 x 256
+    tile with its waves 2 x 4, Q4_K with them 4 x 2.  Checked
     against an fp32 matmul of the GPU-dequantized weights (pinned bit-exact by the dequant
     tests), repeated launches bit-identical, counters back at zero."""
     import gguf_hip
     from gguf_hip.synth import random_shard
 
-    W = random_shard(n, K, G.Q5_K, dev, seed=n + M)
-    wf = gguf_hip.dequantize(W, G.Q5_K, (n, K), torch.float32)
-    gl = gguf_hip.pack_layer([W], [n], [G.Q5_K])
+    W = random_shard(n, K, wt, dev, seed=n + M)
+    wf = gguf_hip.dequantize(W, wt, (n, K), torch.float32)
+    gl = gguf_hip.pack_layer([W], [n], [wt])
     x = torch.randn(M, K, device=dev, generator=torch.Generator(device=dev).manual_seed(M)).to(torch.bfloat16)
     y = gguf_hip.mul_mat_grouped(x, gl)
     ref = x.float() @ wf.T
