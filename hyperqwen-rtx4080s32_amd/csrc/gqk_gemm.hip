@@ -375,37 +375,57 @@ struct GOut {
 
 // Tile geometry: BM tokens x BN weight rows per tile, a WGM x WGN grid of waves each owning
 // (BM / WGM) x (BN / WGN) outputs in 32 x 32 MFMA blocks.  Thread t decodes part t & 1 of weight
-// row t >> 1 each step, and stages AV 16-byte chunks of x.
-template <int BM_, int BN_, int WGM_, int WGN_, int XD_, int WD_>
+// row t >> 1 each step.  x is staged one of two ways: through registers (AV 16-byte chunks per
+// thread, loaded XD steps ahead, stored to padded LDS rows), or with XDMA by direct-to-LDS loads
+// (global_load_lds_dwordx4: a wave's instruction writes 1 KiB of LDS, 16 bytes per lane in lane
+// order) one step ahead into dense 128-byte token rows whose 16-byte chunks are XOR-swizzled.
+template <int BM_, int BN_, int WGM_, int WGN_, int XD_, int WD_, bool XDMA_ = false>
 struct Geo {
   static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, NW = WGM * WGN, NT = 64 * NW;
-  // pipeline depth: x loaded XD steps, weights WD steps before the step that multiplies them
+  // pipeline depth: x loaded XD steps, weights WD steps before the step that multiplies them.
+  // XD >= 2 also moves half of each step's LDS stores to mid-step (the buffer they fill was last
+  // read before the previous barrier, and x two steps ahead is already in registers there).
   static constexpr int XD = XD_, WD = WD_, U = XD * WD / std::gcd(XD, WD);   // steps per unrolled trip
   static_assert(XD >= 1 && XD <= 3 && WD >= 2 && WD <= 3 && (U == 2 || U == 3 || U == 6), "pipeline depths");
+  static constexpr bool XDMA = XDMA_;
   static constexpr int MB = BM / WGM / 32, NB = BN / WGN / 32;   // 32 x 32 blocks per wave
-  static constexpr int AV = BM * 8 / NT;                          // x chunks per thread per step
+  static constexpr int AV = BM * 8 / NT;                          // x chunks per thread per step (registers)
+  static constexpr int XI = BM * GB_K * 2 / 1024 / NW;            // 1 KiB x loads per wave per step (XDMA)
+  static constexpr int XLD = XDMA ? GB_K : GB_LD;                 // LDS x row stride in bf16
   static constexpr int CH = MB * NB * 4;                          // 16-byte accumulator chunks per thread
   static constexpr int SLOT = BM * BN;                            // floats per partial slot
-  static constexpr int LDS = 2 * (BM + BN) * GB_LD * 2;           // double-buffered x and weights
+  static constexpr int LDS = 2 * (BM * XLD + BN * GB_LD) * 2;     // double-buffered x and weights
   static constexpr int WPE = BM <= 32 ? 3 : 2;                    // waves per SIMD kept resident
   static_assert(BN * 2 == NT, "one thread per (weight row, part)");
   static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
+  static_assert(!XDMA || (XI >= 1 && XI * NW * 8 == BM), "whole 8-row x loads per wave");
 };
 // (x / weight prefetch depths of 2 / 2, 3 / 3 and 1 / 3 for the two smaller forms measured the
 // same as 1 / 2 within noise.)
-typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;    // M > 128: 8 waves, one workgroup per CU
-typedef Geo<128, 128, 2, 2, 1, 2> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
-typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;   // 33..64 tokens
-typedef Geo<32, 128, 1, 4, 1, 2> GeoTiny;    // 17..32 tokens: 4 waves side by side, three workgroups per CU
+typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;          // M > 128: 8 waves, one workgroup per CU
+typedef Geo<128, 128, 2, 2, 1, 2, true> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
+typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;         // 33..64 tokens
+typedef Geo<32, 128, 1, 4, 1, 2> GeoTiny;          // 17..32 tokens: 4 waves side by side, three workgroups per CU
+// x by direct-to-LDS loads (XDMA), measured against the register path on both 34816 x 5120 and
+// 5120 x 17408 shards for all eleven types: the 128 x 128 form 1-13% faster at M = 100 (every
+// type but Q5_0, even there); the 256 x 256 form 3-7% faster for Q3_K, Q4_K and IQ4_NL at
+// M = 512 / 2048 and 1-6% slower for Q4_0, Q5_0, Q8_0, Q2_K and Q6_K; the 64 x 128 and 32 x 128
+// forms even to 2-7% slower.  The direct loads go one step ahead (the register path's big form
+// two), and the compiler completes them with a vmcnt(0) at the step's barrier, which also waits
+// for the weight loads in flight; a variant that issued them from inline asm (no compiler wait)
+// with weights three steps ahead measured no faster.
 // The 256 x 256 tile with its 8 waves 2 x 4 (128 tokens x 64 rows each) instead of 4 x 2: the
 // same fragment reads per step, another LDS access and register schedule.  Measured on both
 // 34816 x 5120 and 5120 x 17408 shards at M = 512 / 2048 / 8192, it is 2-7% faster for Q5_0,
 // Q5_K, Q6_K and IQ4_XS and 1-5% slower for Q4_0, Q8_0, Q3_K, Q4_K, IQ4_NL and IQ3_S (Q2_K
 // even), so each type takes the faster grid.  A 8 x 1 grid was slower for every type tried.
 typedef Geo<256, 256, 2, 4, 2, 2> GeoBigWide;
+typedef Geo<256, 256, 4, 2, 2, 2, true> GeoBigDma;
 template <class GE, int T> struct geo_of { typedef GE type; };
 template <int T> struct geo_of<GeoBig, T> {
-  typedef std::conditional_t<T == GQK_Q5_0 || T == GQK_Q5_K || T == GQK_Q6_K || T == GQK_IQ4_XS, GeoBigWide, GeoBig> type;
+  typedef std::conditional_t<T == GQK_Q5_0 || T == GQK_Q5_K || T == GQK_Q6_K || T == GQK_IQ4_XS, GeoBigWide,
+                             std::conditional_t<T == GQK_Q3_K || T == GQK_Q4_K || T == GQK_IQ4_NL, GeoBigDma, GeoBig>>
+      type;
 };
 
 template <int S, class V>
@@ -434,9 +454,21 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
   const int br = tid >> 1, h = tid & 1;
   const int btile = br >> 6, brow = br & 63;
   const uint8_t* bbase = packed + off + (tile0 + (btile < ntiles ? btile : 0)) * nb * (int64_t)(64 * REC);
-  // activation role: AV consecutive 16-byte chunks (8 k each) of token ar
+  // activation role (registers): AV consecutive 16-byte chunks (8 k each) of token ar
   const int ar = tid * AV / 8, ac = (tid * AV) % 8;
   const uint16_t* abase = x + (int64_t)min(m0 + ar, M - 1) * ldx + 8 * ac;
+  // activation role (XDMA): load i of wave w fills token rows 8 (w XI + i) .. + 7 of the step's x
+  // buffer; lane l writes row 8 (w XI + i) + l / 8, chunk slot l % 8, with the k-chunk
+  // (l % 8) ^ swz(row), swz(row) = (row >> 1) & 7: the 16 rows a ds_read_b128 quarter-wave reads
+  // at one k-chunk then fall in 16 distinct 16-byte bank groups of the 256-byte bank width.
+  const uint16_t* xsrc[GE::XDMA ? GE::XI : 1];
+  if constexpr (GE::XDMA) {
+#pragma unroll
+    for (int i = 0; i < GE::XI; ++i) {
+      const int row = 8 * (wave * GE::XI + i) + (lane >> 3);
+      xsrc[i] = x + (int64_t)min(m0 + row, M - 1) * ldx + 8 * ((lane & 7) ^ ((row >> 1) & 7));
+    }
+  }
 
   v16f acc[MB][NB];
 #pragma unroll
@@ -469,6 +501,15 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
     v4u* as = (v4u*)(As + (buf * GE::BM + ar) * GB_LD + 8 * ac);
 #pragma unroll
     for (int i = 0; i < AV; ++i) as[i] = pick<decltype(S)::value>(x0, x1, x2).v[i];
+  };
+  // XDMA: step s's x into LDS buffer buf (the LDS address is wave-uniform; the hardware adds
+  // 16 bytes per lane).  Complete at the s_waitcnt vmcnt(0) before the step's barrier.
+  auto xdma = [&](int buf, int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < GE::XI; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[i] + (int64_t)s * GB_K),
+                                       (__attribute__((address_space(3))) void*)(As + (buf * GE::BM + 8 * (wave * GE::XI + i)) * GB_K),
+                                       16, 0, 0);
   };
   auto wload = [&](auto S, int s) __attribute__((always_inline)) {
     pick<decltype(S)::value>(w0, w1, w2).load(bbase + (int64_t)(s >> 2) * (64 * REC), brow, s & 3, h);
@@ -505,17 +546,23 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
   auto step = [&](auto J, int s) __attribute__((always_inline)) {
     constexpr int j = decltype(J)::value;
     const int buf = (s - k0) & 1;
-    xload(std::integral_constant<int, j % XD>{}, min(s + XD, last));
+    if constexpr (GE::XDMA) {
+      if (s + 1 < k1) xdma(buf ^ 1, s + 1);
+    } else {
+      xload(std::integral_constant<int, j % XD>{}, min(s + XD, last));
+    }
     wload(std::integral_constant<int, j % WD>{}, min(s + WD, last));
-    const uint16_t* as = As + (buf * GE::BM + wm * WTM + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    const uint16_t* as = As + (buf * GE::BM + wm * WTM + (lane & 31)) * GE::XLD + (GE::XDMA ? 0 : 8 * (lane >> 5));
     const uint16_t* bs = Bs + (buf * GE::BN + wn * WTN + (lane & 31)) * GB_LD + 8 * (lane >> 5);
+    const int swz = ((lane & 31) >> 1) & 7;   // XDMA row swizzle: the same for every 32-row block
     uint32_t o[16];
     GS st;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       v8bf af[MB], bf[NB];
 #pragma unroll
-      for (int i = 0; i < MB; ++i) af[i] = *(const v8bf*)(as + 32 * i * GB_LD + 16 * kk);
+      for (int i = 0; i < MB; ++i)
+        af[i] = *(const v8bf*)(as + 32 * i * GE::XLD + (GE::XDMA ? 8 * ((2 * kk + (lane >> 5)) ^ swz) : 16 * kk));
 #pragma unroll
       for (int j2 = 0; j2 < NB; ++j2) bf[j2] = *(const v8bf*)(bs + 32 * j2 * GB_LD + 16 * kk);
 #pragma unroll
@@ -532,33 +579,39 @@ __device__ __forceinline__ void gemm_tile_sk(const uint8_t* __restrict__ packed,
       if constexpr (XD >= 2) {
         if (kk == 1) {
           wstore_half(o, buf ^ 1, std::integral_constant<int, 0>{});
-          xstore(std::integral_constant<int, (j + 1) % XD>{}, buf ^ 1);
+          if constexpr (!GE::XDMA) xstore(std::integral_constant<int, (j + 1) % XD>{}, buf ^ 1);
         }
       }
     }
     if constexpr (XD >= 2) {
       wstore_half(o, buf ^ 1, std::integral_constant<int, 1>{});
     } else {
-      xstore(std::integral_constant<int, (j + 1) % XD>{}, buf ^ 1);
+      if constexpr (!GE::XDMA) xstore(std::integral_constant<int, (j + 1) % XD>{}, buf ^ 1);
       wstore(o, buf ^ 1);
     }
+    if constexpr (GE::XDMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's x loads are in LDS
     __syncthreads();
   };
 
-  xload(std::integral_constant<int, 0>{}, k0);
-  if constexpr (XD > 1) xload(std::integral_constant<int, 1>{}, min(k0 + 1, last));
-  if constexpr (XD > 2) xload(std::integral_constant<int, 2>{}, min(k0 + 2, last));
+  if constexpr (GE::XDMA) {
+    xdma(0, k0);
+  } else {
+    xload(std::integral_constant<int, 0>{}, k0);
+    if constexpr (XD > 1) xload(std::integral_constant<int, 1>{}, min(k0 + 1, last));
+    if constexpr (XD > 2) xload(std::integral_constant<int, 2>{}, min(k0 + 2, last));
+  }
   wload(std::integral_constant<int, 0>{}, k0);
   wload(std::integral_constant<int, 1>{}, min(k0 + 1, last));
   if constexpr (WD > 2) wload(std::integral_constant<int, 2>{}, min(k0 + 2, last));
   {
     uint32_t o[16];
-    xstore(std::integral_constant<int, 0>{}, 0);
+    if constexpr (!GE::XDMA) xstore(std::integral_constant<int, 0>{}, 0);
     const GS st = wprep(std::integral_constant<int, 0>{}, k0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) wdecode(std::integral_constant<int, 0>{}, st, k0, o, i);
     wstore(o, 0);
   }
+  if constexpr (GE::XDMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   // U = lcm(XD, WD) steps per trip, so every set index is a constant; then the last k1 - s < U
   int s = k0;
@@ -704,7 +757,7 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(GE::WPE)
                                                           int G, int gsk) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[GE::LDS + GB_TAB_BYTES + 16];
   uint16_t* As = (uint16_t*)lds;
-  uint16_t* Bs = As + 2 * GE::BM * GB_LD;
+  uint16_t* Bs = As + 2 * GE::BM * GE::XLD;
   int* flag = (int*)(lds + GE::LDS + GB_TAB_BYTES);
   GTabs tb;
 #pragma unroll

@@ -446,14 +446,15 @@ def test_baseline_config1_q8_0(dev):
                                    (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120),
                                    (1000, 2048, 20), (5120, 5120, 32), (200000, 256, 30)],
                          ids=str)
-@pytest.mark.parametrize("wt", [G.Q5_K, G.Q4_K], ids=lambda t: G.NAMES[t])
+@pytest.mark.parametrize("wt", [G.Q5_K, G.Q4_K, G.Q8_0], ids=lambda t: G.NAMES[t])
 def test_gemm_stream_k_schedule(dev, n, K, M, wt):
     """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows; 128 x 128, 64 x 128 and
     32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
     tiles' k-steps split over up to all of them (stream-K, >= 16 steps each, <= 6 per tile) and
     combined in k order by the last contributor.  Small grids are all remainder; the 16384-row
-    case at M=1100 and the 70000- and 200000-row cases mix both phases.  Q5_K runs the 256 x 256
-    tile with its waves 2 x 4, Q4_K with them 4 x 2.  Checked
+    case at M=1100 and the 70000- and 200000-row cases mix both phases.  The 256 x 256 tile runs
+    with its waves 2 x 4 for Q5_K, 4 x 2 with x staged by direct-to-LDS loads for Q4_K and 4 x 2
+    with x through registers for Q8_0; the 128 x 128 form stages x by direct loads.  Checked
     against an fp32 matmul of the GPU-dequantized weights (pinned bit-exact by the dequant
     tests), repeated launches bit-identical, counters back at zero."""
     import gguf_hip
