@@ -1,4 +1,4 @@
-// gqk_gemm.hip - the grouped dequant-GEMM (batch rows M > 32, the prefill regime).
+// gqk_gemm.hip - the grouped dequant-GEMM (batch rows M > 16, the prefill regime).
 //
 // Replaces the reference's prefill paths: the wide int8 forms of the grouped kernel and, for
 // Q4_K / Q5_K, dequantize_tiles + cuBLAS bf16 (gguf-plugin/gluon/interface.py:159-188,
@@ -60,12 +60,14 @@ __device__ __forceinline__ const uint8_t* col16(const uint8_t* plane, int r, int
 
 // ---- tile forms ------------------------------------------------------------------------------
 // A workgroup owns BM tokens x BN weight rows (BN / 64 tiles of one shard) and walks K in steps of
-// 64.  Forms: 256 x 256 with 8 waves (two per SIMD, one workgroup per CU: M > 128), and 128 x 128 /
-// 64 x 128 with 4 waves (two workgroups per CU: M 65..128 / 33..64).  Each wave owns a block of
+// 64.  Forms: 256 x 256 with 8 waves (two per SIMD, one workgroup per CU: M > 128), 128 x 128 /
+// 64 x 128 with 4 waves (two workgroups per CU: M 65..128 / 33..64) and 32 x 128 with 4 waves side
+// by side (three workgroups per CU: M 17..32).  Each wave owns a block of
 // 32 x 32 v_mfma_f32_32x32x16_bf16 outputs.  Per step each thread decodes 32 weights of one row
-// (two runs of 16 at step-local offsets OFF0 / OFF1, per type) and stages activations of one
-// token; the next steps' loads are in flight during the MFMAs.  LDS: x and weights
-// double-buffered plus the IQ3_S tables.
+// (two runs of 16 at step-local offsets OFF0 / OFF1, per type) and, in the forms that stage x
+// through registers, stores activations of one token (the others load x straight into LDS); the
+// next steps' loads are in flight during the MFMAs.  LDS: x and weights double-buffered plus the
+// IQ3_S tables.
 
 #define GQK_GB_WORD3 0x00020000   // buffer resource word 3: raw untyped dword access
 #define GQK_GB_SC1 16             // device-scope cache policy (write through / bypass the XCD L2)
