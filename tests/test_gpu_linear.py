@@ -473,3 +473,28 @@ def test_gemm_stream_k_schedule(dev, n, K, M, wt):
     torch.cuda.synchronize()
     info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[:gguf_hip.ops._NPLAN])
     assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0    # the arrival counters
+
+
+@pytest.mark.parametrize("wt", [G.Q4_K, G.Q6_K, G.Q8_0], ids=lambda t: G.NAMES[t])
+def test_strided_activations_every_form(dev, wt):
+    """x as a column slice of a wider buffer (row stride K + 24, 16-byte aligned start) goes to the
+    kernels as is, in every form: GEMV (M <= 16) and the four GEMM tiles, with x staged through
+    registers (Q6_K, Q8_0 in the 256 x 256 form) or by direct-to-LDS loads (the 128 x 128 form,
+    Q4_K in the 256 x 256 form), full and partial token blocks.  Each result is bit-identical to
+    the one from a contiguous copy of x."""
+    import gguf_hip
+    from gguf_hip.synth import random_shard
+
+    n, K = 300, 2048
+    W = random_shard(n, K, wt, dev, seed=77 + wt)
+    gl = gguf_hip.pack_layer([W], [n], [wt])
+    wf = gguf_hip.dequantize(W, wt, (n, K), torch.float32)
+    for M in (8, 20, 48, 100, 256, 300):
+        big = torch.randn(M, K + 24, device=dev, generator=torch.Generator(device=dev).manual_seed(M)).to(torch.bfloat16)
+        xs = big[:, 8:8 + K]
+        assert xs.stride(0) == K + 24 and xs.data_ptr() % 16 == 0
+        y = gguf_hip.mul_mat_grouped(xs, gl)
+        assert torch.equal(y, gguf_hip.mul_mat_grouped(xs.contiguous(), gl)), (G.NAMES[wt], M)
+        ref = xs.float() @ wf.T
+        e = float(((y.float() - ref).abs() / ref.abs().amax(dim=1, keepdim=True).clamp(min=1e-30)).amax())
+        assert e < TOL, (G.NAMES[wt], M, e)
