@@ -105,7 +105,8 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
  * enough, the descriptor table (16 int32 per row) to upload to the device.  target_wgs > 0
  * overrides the GEMV heuristic's target of resident waves (0 = default: eight per CU of the
  * device current at the call, 256 CUs assumed when none is visible), from which the waves per
- * workgroup and the split-K factor follow.  Replaces
+ * workgroup and the split-K factor follow.  GEMM plans (M > 16) take their tile form from M and,
+ * at 129..384 rows, from the layer's size against the same device's CU count.  Replaces
  * prepare_grouped_layer / descriptors / grouped_split_for
  * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
 int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,

@@ -448,8 +448,9 @@ def test_baseline_config1_q8_0(dev):
                          ids=str)
 @pytest.mark.parametrize("wt", [G.Q5_K, G.Q4_K, G.Q8_0], ids=lambda t: G.NAMES[t])
 def test_gemm_stream_k_schedule(dev, n, K, M, wt):
-    """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows; 128 x 128, 64 x 128 and
-    32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
+    """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows, except 129..384 rows of a
+    layer with few 256-row groups, which keep 128 x 128 (1000 rows at M = 300 here); 128 x 128,
+    64 x 128 and 32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
     tiles' k-steps split over up to all of them (stream-K, >= 16 steps each, <= 6 per tile) and
     combined in k order by the last contributor.  Small grids are all remainder; the 16384-row
     case at M=1100 and the 70000- and 200000-row cases mix both phases.  The 256 x 256 tile runs
