@@ -851,12 +851,14 @@ static int gb_slot_floats(int bm) {
 }
 
 // Stream-K workgroups for R remainder tiles of S = 4 nb steps: at most G, at least 16 steps per
-// workgroup and at most 6 workgroups per tile.  The last contributor of a tile sums every other
-// one's partial slot in dependent device-scope round trips, so contributors cost more than the
-// steps they take over: measured on the 5120-row shards at M = 17..200, all G workgroups (13
-// per tile) took 33-110 us, 16 steps / <= 6 per tile 22-70 us; tile-rich shards keep all G.
-static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb) {
-  return std::max<int64_t>(1, std::min<int64_t>({(int64_t)G, R * 4 * nb / 16, 6 * R}));
+// workgroup and at most 6 workgroups per tile (12 in the 32 x 128 form, whose partial tiles are
+// small).  The last contributor of a tile sums every other one's partial slot in dependent
+// device-scope round trips, so contributors cost more than the steps they take over: measured on
+// the 5120-row shards at M = 17..200, all G workgroups (13 per tile) took 33-110 us, 16 steps /
+// <= 6 per tile 22-70 us; tile-rich shards keep all G.  Up to 12 per tile: `down` (K = 17408) at
+// M = 20-32 4-6% faster, at M = 48-100 (the larger forms) 1-20% slower.
+static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb, int bm) {
+  return std::max<int64_t>(1, std::min<int64_t>({(int64_t)G, R * 4 * nb / 16, (bm == 32 ? 12 : 6) * R}));
 }
 
 // Workspace: ctr_bytes of counters (the plan's counter region: at least G ints), then the partial tiles.
@@ -866,7 +868,7 @@ int64_t gemm_workspace(int bm, int n_desc, int M, int nb, int64_t ctr_bytes) {
   const int64_t T = (int64_t)n_desc * ((M + bm - 1) / bm);
   const int64_t R = T % G;
   if (R == 0) return 0;
-  const int64_t gsk = gb_stream_k_workgroups(G, R, nb);
+  const int64_t gsk = gb_stream_k_workgroups(G, R, nb, bm);
   return ctr_bytes + (R + gsk - 1) * gb_slot_floats(bm) * 4;
 }
 
@@ -895,7 +897,7 @@ static int launch_sk(int only, int n_desc, int M, int nb, hipStream_t st, const 
   float* part = need > 0 ? (float*)((char*)ws + ctr_bytes) : nullptr;
   // G workgroups when there are at least G tiles; else the stream-K participants only
   const int64_t T = (int64_t)n_desc * ((M + GE::BM - 1) / GE::BM);
-  const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb);
+  const int gsk = (int)gb_stream_k_workgroups(G, T % G, nb, GE::BM);
   dim3 grid((unsigned)(T >= G ? G : gsk));
   switch (only) {
 #define C(T) case T: hipLaunchKernelGGL((gemm_sk_kernel<typename geo_of<GE, T>::type, T>), grid, dim3(GE::NT), 0, st, packed, desc, n_desc, x, ldx, M, y, ldy, bias, part, ctr, G, gsk); return GQK_OK;
