@@ -338,13 +338,14 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // 32 / 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens
     // on the GEMM outruns the GEMV's 4 x 4 x 4 MFMAs (one decode of each weight for up to 128 tokens).
     pi.bm = M <= 32 ? 32 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
-    // A layer with few 256-row groups keeps the 128 x 128 form up to 384 rows (512 for K up to
+    // A layer with few 256-row groups keeps the 128 x 128 form up to 384 rows (768 for K up to
     // 8192) when the 256 x 256 form would have fewer tiles than a quarter of the CUs (one
     // workgroup each): its stream-K would leave most CUs idle and pad the last token block.
     // Measured on the 5120- and 7168-row shards (20 / 28 groups of 256 rows): 13-30% faster at
-    // M = 129-384, 9-19% at 448-512 for K = 5120; `down` (K = 17408) 5-19% slower at 448-512,
-    // and gate_up (136 groups) 6-22% slower at every M.
-    if (pi.bm == 256 && (M <= 384 || (M <= 512 && nb <= 32))) {
+    // M = 129-384, 9-19% at 448-512 and (o_proj) 6-21% at 640-768 for K = 5120; qkv at 640-768
+    // (above the quarter) even to 11% slower, `down` (K = 17408) 5-19% slower at 448-512, and
+    // gate_up (136 groups) 6-22% slower at every M.
+    if (pi.bm == 256 && (M <= 384 || (M <= 768 && nb <= 32))) {
       int64_t groups = 0;
       for (int i = 0; i < nshards; ++i) groups += ((shards[i].n + 63) / 64 + 3) / 4;
       if (groups * ((M + 255) / 256) * 4 < current_cus()) pi.bm = 128;

@@ -34,9 +34,9 @@ UNQUANTIZED_TYPES = (0, 1, 30)
 
 # batch-row buckets of a grouped layer: GEMV plans serve M <= 4, 8, 16; GEMM above
 GEMV_BUCKETS = (4, 8, 16)
-# GEMM plans: 32 / 64 x 128 tiles (17..32 / 33..64 rows), 128 x 128 (65..128), 129..384 and 385..512
-# (256 x 256, or 128 x 128 for a layer with few 256-row groups), 256 x 256 above
-GEMM_PLAN_M = (32, 64, 128, 384, 512, 513)
+# GEMM plans: 32 / 64 x 128 tiles (17..32 / 33..64 rows), 128 x 128 (65..128), 129..384, 385..512 and
+# 513..768 (256 x 256, or 128 x 128 for a layer with few 256-row groups), 256 x 256 above
+GEMM_PLAN_M = (32, 64, 128, 384, 512, 768, 769)
 
 _DTYPES = {torch.float32: _lib.GQK_DTYPE_F32, torch.bfloat16: _lib.GQK_DTYPE_BF16, torch.float16: _lib.GQK_DTYPE_F16}
 

@@ -253,7 +253,7 @@ def test_plan_random_layers_stay_in_bounds():
                 assert all(int(r[6]) - int(r[5]) >= info.nw for r in d), case
         else:
             groups = sum(((n + 63) // 64 + 3) // 4 for _, n, _ in shards)
-            short = M <= 384 or (M <= 512 and K <= 32 * 256)
+            short = M <= 384 or (M <= 768 and K <= 32 * 256)
             big = 256 if not short or groups * ((M + 255) // 256) * 4 >= 256 else 128
             assert info.form == 2 and info.bm == (32 if M <= 32 else 64 if M <= 64 else 128 if M <= 128 else big)
             per = 4 if info.bm == 256 else 2
@@ -313,7 +313,8 @@ def test_plan_buckets():
     assert ops._pick_plan([], 64) == 4 and ops._pick_plan([], 65) == 5 and ops._pick_plan([], 128) == 5
     assert ops._pick_plan([], 129) == 6 and ops._pick_plan([], 384) == 6
     assert ops._pick_plan([], 385) == 7 and ops._pick_plan([], 512) == 7
-    assert ops._pick_plan([], 513) == 8 and ops._pick_plan([], 8192) == 8
+    assert ops._pick_plan([], 513) == 8 and ops._pick_plan([], 768) == 8
+    assert ops._pick_plan([], 769) == 9 and ops._pick_plan([], 8192) == 9
     # every type, the table types (IQ4_NL / IQ4_XS / IQ3_S) included, stays on the GEMV up to 16 rows
     for wt in (20, 23, 21):
         i9, i16, i17 = (ops.plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17))
@@ -321,7 +322,7 @@ def test_plan_buckets():
     off = ops.tiles_bytes(12, 512, 512)
     assert ops.plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 1
     for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 128), (384, 128),
-                  (512, 128), (513, 256), (2048, 256)):
+                  (512, 128), (768, 128), (769, 256), (2048, 256)):
         assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm
     # 129..384 rows: 256 x 256 tiles once the 256-row groups times the token blocks reach a quarter
     # of the CUs (256 assumed without a GPU): 34816 rows = 136 groups, 16384 = 64, 16000 = 63,
@@ -329,9 +330,11 @@ def test_plan_buckets():
     for n, M, bm in ((34816, 129, 256), (34816, 384, 256), (7168, 256, 128), (7168, 384, 128),
                      (5120, 384, 128), (16000, 256, 128), (16000, 257, 256), (16384, 129, 256)):
         assert ops.plan([(12, n, 0)], 512, M)[0].bm == bm, (n, M)
-    # 385..512 rows only for K up to 8192 (32 super-blocks)
-    for K, M, bm in ((5120, 512, 128), (8192, 512, 128), (8448, 512, 256), (17408, 448, 256), (17408, 384, 128)):
+    # 385..768 rows only for K up to 8192 (32 super-blocks)
+    for K, M, bm in ((5120, 512, 128), (8192, 512, 128), (8448, 512, 256), (17408, 448, 256), (17408, 384, 128),
+                     (5120, 768, 128), (5120, 769, 256)):
         assert ops.plan([(12, 5120, 0)], K, M)[0].bm == bm, (K, M)
+    assert ops.plan([(12, 7168, 0)], 5120, 640)[0].bm == 256       # 28 groups x 3 blocks: above the quarter
 
 
 def test_ggml_dequantize_rejects_rows_narrower_than_n():
