@@ -634,16 +634,149 @@ __host__ __device__ constexpr int gemv_lds_bytes(int nw, bool tables) {
 // a fixed order.  A tile covered by one row (D_NC = 1) is written to y; a tile shared by D_NC rows
 // (split-K) sends its fp32 partial to slot D_SLOT0 + D_SPLIT, and the last workgroup of the tile
 // to arrive (counter ctr[D_CTR]) sums the partials in split order, writes y and resets the counter.
-// Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 and
-// IQ3_S at G = 4 fit three waves without spilling and run faster there than at the allocator's
-// own choice of two (IQ3_S gate_up at M = 12 / 16: ~10%, down even).  Q6_K at G = 4 measured
-// 0-8% faster on gate_up and 2-4% slower on down at three; IQ4_NL, IQ4_XS and Q8_0 spill there.
+typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
+typedef unsigned v2u_t __attribute__((ext_vector_type(2)));
+typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+// 4 x 4 transpose of 16-lane groups across four registers: out[b] at lane 16 c + r = in[c] at
+// lane 16 b + r (v_permlane32_swap, then v_permlane16_swap).
+__device__ __forceinline__ void xpose4(uint32_t& a0, uint32_t& a1, uint32_t& a2, uint32_t& a3) {
+  const v2u_t p = __builtin_amdgcn_permlane32_swap(a0, a2, false, false);
+  const v2u_t q = __builtin_amdgcn_permlane32_swap(a1, a3, false, false);
+  const v2u_t u = __builtin_amdgcn_permlane16_swap(p[0], q[0], false, false);
+  const v2u_t w = __builtin_amdgcn_permlane16_swap(p[1], q[1], false, false);
+  a0 = u[0]; a1 = u[1]; a2 = w[0]; a3 = w[1];
+}
+__device__ __forceinline__ void xpose4f(float& a0, float& a1, float& a2, float& a3) {
+  uint32_t b0 = __builtin_bit_cast(uint32_t, a0), b1 = __builtin_bit_cast(uint32_t, a1);
+  uint32_t b2 = __builtin_bit_cast(uint32_t, a2), b3 = __builtin_bit_cast(uint32_t, a3);
+  xpose4(b0, b1, b2, b3);
+  a0 = __builtin_bit_cast(float, b0); a1 = __builtin_bit_cast(float, b1);
+  a2 = __builtin_bit_cast(float, b2); a3 = __builtin_bit_cast(float, b3);
+}
+// Types that take the 16 x 16 x 32 form at G = 4 (9-16 rows).  Measured against the 4 x 4 x 4 form
+// on gate_up, down, qkv and o_proj at M = 12 / 16 (three rotating copies): IQ4_NL 8-14% faster,
+// IQ4_XS 1-16%, IQ3_S 0-13%, Q8_0 0-8%, Q4_0 3-5% and Q5_0 -4..+4%; Q4_K even and Q5_K 1-6% slower,
+// so those two keep the 4 x 4 x 4 form.  At G = 8 (17-32 rows) the form was 3-36% slower than the
+// 32 x 128 GEMM for most types and shards.
+template <int G, int T>
+constexpr bool w16() {
+  return G == 4 && (T == GQK_Q4_0 || T == GQK_Q5_0 || T == GQK_Q8_0 || T == GQK_IQ4_NL || T == GQK_IQ3_S ||
+                    T == GQK_IQ4_XS);
+}
+
+// A operand of one 32-weight group for lane (token, chunk c): 8 bf16 of x in the decoder's slot
+// order for slots 2c, 2c + 1 (FAM_NAT: k 8c..8c+7; FAM_SWAP: pairs (4m, 4m+2), (4m+1, 4m+3);
+// FAM_IQ4: (2m, 2m+16), (2m+1, 2m+17)).
+template <int FAM>
+__device__ __forceinline__ v4u_t w16_a(const uint16_t* xr, int c) {
+  if constexpr (FAM == FAM_IQ4) {   // slots (2m, 2m+16, 2m+1, 2m+17): k 4c..4c+3 interleaved with 16+4c..
+    const uint2 lo = *(const uint2*)(xr + 4 * c), hi = *(const uint2*)(xr + 16 + 4 * c);
+    return v4u_t{__builtin_amdgcn_perm(hi.x, lo.x, 0x05040100u), __builtin_amdgcn_perm(hi.x, lo.x, 0x07060302u),
+                 __builtin_amdgcn_perm(hi.y, lo.y, 0x05040100u), __builtin_amdgcn_perm(hi.y, lo.y, 0x07060302u)};
+  } else {
+    const uint4 a = *(const uint4*)(xr + 8 * c);
+    if constexpr (FAM == FAM_SWAP)   // (4m, 4m+2, 4m+1, 4m+3)
+      return v4u_t{__builtin_amdgcn_perm(a.y, a.x, 0x05040100u), __builtin_amdgcn_perm(a.y, a.x, 0x07060302u),
+                   __builtin_amdgcn_perm(a.w, a.z, 0x05040100u), __builtin_amdgcn_perm(a.w, a.z, 0x07060302u)};
+    else
+      return v4u_t{a.x, a.y, a.z, a.w};
+  }
+}
+
+// The 16 x 16 x 32 form of a wave (32-weight scale groups, 16 tokens per half): one
+// v_mfma_f32_16x16x32_bf16 per row block of 16 rows, token half and group.  x is the A operand,
+// loaded straight from global memory (lane 16 c + t: token t, the 8 weights of slots 2c, 2c + 1 in
+// the decoder's order; no LDS staging); the weights, decoded one row per lane as in the 4 x 4 x 4
+// form, reach the B operand (lane 16 c + r: row 16 b + r) through a 4 x 4 transpose of 16-lane
+// groups, and the scales likewise, so the output lane holds its own row r of block b for tokens
+// 16 h + 4 c .. + 3.  The group sums of x for the bias term come from one more MFMA against ones.
+// acc is returned in the lane-per-row layout of the 4 x 4 x 4 form (a last transpose).
+template <int G, int T>
+__device__ __forceinline__ void gemv_wave_w16(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
+                                              int64_t ldx, int M, int kw0, int kw1, const Tabs& tb, const Masks& mk,
+                                              v4f (&acc)[G]) {
+  typedef Dec<T> D;
+  constexpr int H = G / 4;
+  constexpr bool BIAS = !(T == GQK_IQ4_NL || T == GQK_IQ4_XS || T == GQK_IQ3_S);
+  const int lane = threadIdx.x & 63, lr = lane & 15, lc = lane >> 4;
+  if (kw0 >= kw1) return;
+  const uint16_t* xrow[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) xrow[h] = x + (int64_t)min(16 * h + lr, M - 1) * ldx;
+  const v8bf_t ones = __builtin_bit_cast(v8bf_t, v4u_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+  const int last = kw1 - 1;
+  auto recp = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
+  auto process = [&](const D& rec, int kb) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      v4u_t av[H];
+#pragma unroll
+      for (int h = 0; h < H; ++h) av[h] = w16_a<D::FAM>(xrow[h] + (int64_t)kb * 256 + 32 * s, lc);
+      float sc[4], bi[4];
+      rec.scales(s, sc[0], bi[0]);
+      sc[1] = sc[2] = sc[3] = sc[0];
+      xpose4f(sc[0], sc[1], sc[2], sc[3]);
+      if constexpr (BIAS) {
+        bi[1] = bi[2] = bi[3] = bi[0];
+        xpose4f(bi[0], bi[1], bi[2], bi[3]);
+      }
+      uint32_t P[4][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        rec.pair(s, 2 * c, P[c][0], P[c][1], tb, mk);
+        rec.pair(s, 2 * c + 1, P[c][2], P[c][3], tb, mk);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xpose4(P[0][j], P[1][j], P[2][j], P[3][j]);
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        const v8bf_t A = __builtin_bit_cast(v8bf_t, av[h]);
+        v4f xq = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (BIAS) xq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones, xq, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const v8bf_t B = __builtin_bit_cast(v8bf_t, v4u_t{P[b][0], P[b][1], P[b][2], P[b][3]});
+          const v4f Dm = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, B, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float a = __builtin_fmaf(sc[b], Dm[i], acc[4 * h + b][i]);
+            if constexpr (BIAS) a = __builtin_fmaf(-bi[b], xq[i], a);
+            acc[4 * h + b][i] = a;
+          }
+        }
+      }
+    }
+  };
+  D r0, r1;
+  r0.load(recp(kw0), lane);
+  r1.load(recp(kw0 + 1), lane);
+  for (int kb = kw0;; kb += 2) {
+    process(r0, kb);
+    r0.load(recp(kb + 2), lane);
+    if (kb + 1 > last) break;
+    process(r1, kb + 1);
+    r1.load(recp(kb + 3), lane);
+    if (kb + 2 > last) break;
+  }
+#pragma unroll
+  for (int h = 0; h < H; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a0 = acc[4 * h][i], a1 = acc[4 * h + 1][i], a2 = acc[4 * h + 2][i], a3 = acc[4 * h + 3][i];
+      xpose4f(a0, a1, a2, a3);
+      acc[4 * h][i] = a0; acc[4 * h + 1][i] = a1; acc[4 * h + 2][i] = a2; acc[4 * h + 3][i] = a3;
+    }
+}
+
+// Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 fits
+// three waves without spilling and runs faster there than at the allocator's own choice of two.
+// Q6_K at G = 4 measured 0-8% faster on gate_up and 2-4% slower on down at three.
 template <int G, int ONLY>
 constexpr int gemv_waves() {
 #ifdef GQK_GEMV_WAVES
   return GQK_GEMV_WAVES;
 #else
-  return ((G == 2 && ONLY == GQK_Q6_K) || (G == 4 && ONLY == GQK_IQ3_S)) ? 3 : 1;
+  return (G == 2 && ONLY == GQK_Q6_K) ? 3 : 1;
 #endif
 }
 
@@ -675,8 +808,12 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   for (int g = 0; g < G; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
 
 #define RUN(T)                                                                                           \
-  if ((ONLY == 0 || ONLY == T) && type == T)                                                             \
-    gemv_wave<G, T, ONE>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, wl, tb, mk, acc);
+  if ((ONLY == 0 || ONLY == T) && type == T) {                                                           \
+    if constexpr (w16<G, T>())                                                                           \
+      gemv_wave_w16<G, T>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, tb, mk, acc); \
+    else                                                                                                 \
+      gemv_wave<G, T, ONE>(packed + off + tile * nb * (int64_t)(64 * Dec<T>::REC), x, ldx, M, kw0, kw1, wl, tb, mk, acc); \
+  }
   RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
   RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN

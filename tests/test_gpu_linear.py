@@ -60,7 +60,7 @@ def test_gemv_split_k_ragged(dev, wt):
     W = torch.from_numpy(raw).to(dev)
     for target in (1, 3, 7, 40):
         gl = gguf_hip.pack_layer([W], [n], [wt], target_wgs=target)
-        for M in (1, 7, 32):
+        for M in (1, 7, 12, 32):
             x = _x(M, K, 2000 + M, dev)
             e = G.rel_err(gguf_hip.mul_mat_grouped(x, gl).float().cpu().numpy(), _ref(x, wf))
             assert e < TOL, (G.NAMES[wt], target, M, e)
@@ -476,10 +476,11 @@ def test_gemm_stream_k_schedule(dev, n, K, M, wt):
     assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0    # the arrival counters
 
 
-@pytest.mark.parametrize("wt", [G.Q4_K, G.Q6_K, G.Q8_0], ids=lambda t: G.NAMES[t])
+@pytest.mark.parametrize("wt", [G.Q4_K, G.Q6_K, G.Q8_0, G.IQ4_XS], ids=lambda t: G.NAMES[t])
 def test_strided_activations_every_form(dev, wt):
     """x as a column slice of a wider buffer (row stride K + 24, 16-byte aligned start) goes to the
-    kernels as is, in every form: GEMV (M <= 16) and the four GEMM tiles, with x staged through
+    kernels as is, in every form: GEMV (M <= 16; at 9-16 rows Q8_0 / IQ4_XS read it straight from
+    global memory in the 16 x 16 x 32 form) and the four GEMM tiles, with x staged through
     registers (Q6_K, Q8_0 in the 256 x 256 form) or by direct-to-LDS loads (the 128 x 128 form,
     Q4_K in the 256 x 256 form), full and partial token blocks.  Each result is bit-identical to
     the one from a contiguous copy of x."""
@@ -490,7 +491,7 @@ def test_strided_activations_every_form(dev, wt):
     W = random_shard(n, K, wt, dev, seed=77 + wt)
     gl = gguf_hip.pack_layer([W], [n], [wt])
     wf = gguf_hip.dequantize(W, wt, (n, K), torch.float32)
-    for M in (8, 20, 48, 100, 256, 300):
+    for M in (8, 12, 20, 48, 100, 256, 300):
         big = torch.randn(M, K + 24, device=dev, generator=torch.Generator(device=dev).manual_seed(M)).to(torch.bfloat16)
         xs = big[:, 8:8 + K]
         assert xs.stride(0) == K + 24 and xs.data_ptr() % 16 == 0
