@@ -88,8 +88,9 @@ def test_reference_wide_form_edges(dev, wt):
 def test_config5_mixed_type_layers(dev, layer):
     """BASELINE config 5 at its layer shapes: decoder layers of the seeded 64-layer type draw
     (the one bench_configs.py times), each as one mixed-type grouped launch over qkv 7168 / o_proj
-    5120 / gate_up 34816 rows at K = 5120 plus down 5120 x 17408, at M = 1, 8, 32, 64, 100 (the
-    mixed-type GEMV and every small GEMM form, x staged by direct-to-LDS loads at 100): every
+    5120 / gate_up 34816 rows at K = 5120 plus down 5120 x 17408, at M = 1, 8, 12, 32, 64, 100 (the
+    mixed-type GEMV, with the 16 x 16 x 32 form's types at 12, and every small GEMM form, x staged
+    by direct-to-LDS loads at 100): every
     shard's rows pinned bit-exact against the oracle on a subset, and the launches against an fp32
     matmul of the dequantized weights within 1e-2."""
     import gguf_hip
@@ -110,7 +111,7 @@ def test_config5_mixed_type_layers(dev, layer):
     gld = gguf_hip.pack_layer([Wd], [5120], [t_d])
     del Wd
     g = torch.Generator(device=dev).manual_seed(layer)
-    for M in (1, 8, 32, 64, 100):
+    for M in (1, 8, 12, 32, 64, 100):
         x = torch.randn(M, 5120, device=dev, generator=g).to(torch.bfloat16)
         y = gguf_hip.mul_mat_grouped(x, gl)
         assert y.shape == (M, wf.shape[0])

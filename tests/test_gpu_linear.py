@@ -241,7 +241,7 @@ def test_mixed_layer_one_launch(dev):
     wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
     gl = gguf_hip.pack_layer(Ws, [n for _, n in shards], [wt for wt, _ in shards], target_wgs=1)
     singles = [gguf_hip.pack_layer([W], [n], [wt], target_wgs=1) for W, (wt, n) in zip(Ws, shards)]
-    for M in (1, 6, 20, 40, 200):
+    for M in (1, 6, 12, 20, 40, 200):   # 12: IQ3_S / Q8_0 / IQ4_XS in the 16 x 16 x 32 form beside the others
         x = _x(M, K, 3000 + M, dev)
         y = gguf_hip.mul_mat_grouped(x, gl)
         assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
