@@ -62,19 +62,35 @@ def _capture(fn, torch):
     return g
 
 
-def _traffic(symbol: str, dom: dict, M: int):
+def _source_sha16(rel: str) -> str:
+    import hashlib
+
+    with open(os.path.join(REPO, rel), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def _traffic(symbol: str, dom: dict, M: int) -> tuple[int | None, str]:
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter's reading on a plain copy of
-    known size), or None when no summary matches this kernel and workload."""
+    known size; PMC counters are not read in this run), and where the figure comes from.  A
+    summary counts only for the same kernel symbol and workload, taken from the same kernel
+    source (its recorded sha256 prefix equals the current file's): a kernel changed since the
+    profile gives None, with the reason."""
     path = os.path.join(REPO, "profiles", "traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no profiles/traffic.json"
     with open(path, encoding="utf-8") as f:
         rec = json.load(f)
     for r in rec.get("kernels", []):
         if r.get("symbol") == symbol and r.get("N") == dom["N"] and r.get("K") == dom["K"] and r.get("M") == M:
-            return r["hbm_bytes_per_launch"]
-    return None
+            src = r.get("source")
+            if not src or r.get("source_sha16") != _source_sha16(src):
+                return None, (f"profiles/traffic.json holds {symbol} at this shape, but from another version of "
+                              f"{src or 'its source'}: stale, not used")
+            return r["hbm_bytes_per_launch"], ("profiles/traffic.json: rocprofv3 FETCH_SIZE / WRITE_SIZE of the "
+                                               f"same kernel source ({src} sha256 {r['source_sha16']}), "
+                                               "not measured in this run")
+    return None, f"no PMC summary of {symbol} at this shape in profiles/traffic.json"
 
 
 def cpu_baseline(seconds: float = 15.0) -> dict:
@@ -147,6 +163,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=3, help="rotating weight copies of the step (> 1 GB in total)")
     ap.add_argument("--shard-bytes", type=float, default=320e6,
                     help="per-shard timings rotate at least this many bytes of copies (> the 256 MB Infinity Cache)")
+    ap.add_argument("--extra-m", default="16,32",
+                    help="also time every shard alone at these batch rows (comma-separated; empty: skip)")
+    ap.add_argument("--stack-m", default="1,8,32,64", help="config 5 lines: batch rows (comma-separated)")
     ap.add_argument("--stack-layers", type=int, default=64, help="config 5 lines: decoder layers (0: skip)")
     ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -218,24 +237,43 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # per-shard launch time (graph of every copy, > 256 MB of them, twice; average per launch)
-    rows = []
-    for wt, name, N, K, gls, nb in shards:
+    def shard_us(gls, x):
         reps = max(1, 8 // len(gls))
 
-        def f(gls=gls, K=K, reps=reps):
+        def f():
             for _ in range(reps):
                 for gl in gls:
-                    gguf_hip.mul_mat_grouped(xs[K], gl)
+                    gguf_hip.mul_mat_grouped(x, gl)
         g = _capture(f, torch)
         g.replay()
         t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (reps * len(gls))
-        info = gguf_hip.ops.GqkPlanInfo.from_tuple(
-            gls[0].plans[gguf_hip.ops._pick_plan(gls[0].plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
-        rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(t * 1e3, 2),
-                     "copies": len(gls),
-                     "GBps": round(nb / (t * 1e-3) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
-                     "waves_per_wg": info.nw, "one_record": info.bm == 1})
         del g
+        return t * 1e3
+
+    def plan_of(gl, m):
+        return gguf_hip.ops.GqkPlanInfo.from_tuple(
+            gl.plans[gguf_hip.ops._pick_plan(gl.plans, m) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
+
+    rows = []
+    for wt, name, N, K, gls, nb in shards:
+        us = shard_us(gls, xs[K])
+        info = plan_of(gls[0], M)
+        rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
+                     "copies": len(gls),
+                     "GBps": round(nb / (us * 1e-6) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
+                     "waves_per_wg": info.nw, "one_record": info.bm == 1})
+    # the rest of the metric's range (M = 9..32: speculative rows of several streams)
+    extra = []
+    for Me in [int(v) for v in args.extra_m.split(",") if v]:
+        xe = {K: torch.randn(Me, K, device=dev).to(torch.bfloat16) for K in xs}
+        for wt, name, N, K, gls, nb in shards:
+            us = shard_us(gls, xe[K])
+            info = plan_of(gls[0], Me)
+            gbs = nb / (us * 1e-6) / 1e9
+            extra.append({"M": Me, "type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
+                          "form": "gemv" if info.form == 1 else f"gemm{info.bm}", "GBps": round(gbs, 1),
+                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del xe
     dom = max(rows, key=lambda r: r["us"])
     dom_wt = next(s[0] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
     dom_w = next(s[5] for s in shards if gguf_hip.TYPE_NAMES[s[0]] == dom["type"] and s[1] == dom["shard"])
@@ -245,7 +283,7 @@ def main() -> int:
     # the kernel's template arguments: token groups, type, and whether it is the build without the
     # register pipeline (plans whose waves all stream one record)
     dom_symbol = f"gqk::gemv_kernel<{dom['g']}, {dom_wt}, {'true' if dom['one_record'] else 'false'}>"
-    traffic = _traffic(dom_symbol, dom, M)
+    traffic, traffic_source = _traffic(dom_symbol, dom, M)
     if args.detail:
         for r in rows:
             print(json.dumps(r), file=sys.stderr)
@@ -273,19 +311,28 @@ def main() -> int:
         from bench_configs import build_stack, time_stack
         del shards, xs
         torch.cuda.empty_cache()
-        grouped, _, stack_bytes, _ = build_stack(torch, gguf_hip, random_shard, dev, args.stack_layers)
+        grouped, per_linear, stack_bytes, _ = build_stack(torch, gguf_hip, random_shard, dev, args.stack_layers)
         stack = {"workload": f"BASELINE config 5: {args.stack_layers} decoder layers (seeded type draw over the eleven "
-                             "types), one mixed-type grouped launch per layer over qkv/o_proj/gate_up at K=5120 plus "
-                             "one for down", "packed_bytes": stack_bytes,
+                             "types weighted toward Q4_K / Q5_K / IQ4_XS), the weight stream of one decode step",
+                 "packed_bytes": stack_bytes,
                  "bpw": round(8 * stack_bytes / (args.stack_layers * sum(N * K for _, N, K in SHAPES)), 3),
+                 "schedules": {
+                     "per_linear": "the reference's schedule: one grouped launch per linear module (qkv, o_proj, "
+                                   "gate_up, down: 4 per decoder layer, as the plugin's _create_groups groups "
+                                   "each module's shards), each on its own input",
+                     "grouped": "one mixed-type launch per layer over qkv + o_proj + gate_up (K = 5120) plus one "
+                                "for down, on a single x: a weight-stream bound that a decoder cannot issue "
+                                "(o_proj reads the attention output and gate_up the post-attention norm)"},
                  "lines": []}
-        for Ms in (1, 8):
-            t = time_stack(torch, gguf_hip, dev, grouped, Ms)
-            gbs = stack_bytes / (t * 1e-3) / 1e9
-            stack["lines"].append({"M": Ms, "ms_per_step": round(t, 4), "GBps": round(gbs, 1),
-                                   "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                                                "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}})
-        del grouped
+        for Ms in [int(v) for v in args.stack_m.split(",") if v]:
+            for sched, lst in (("per_linear", per_linear), ("grouped", grouped)):
+                t = time_stack(torch, gguf_hip, dev, lst, Ms)
+                gbs = stack_bytes / (t * 1e-3) / 1e9
+                stack["lines"].append({"schedule": sched, "M": Ms, "launches_per_step": len(lst),
+                                       "ms_per_step": round(t, 4), "GBps": round(gbs, 1),
+                                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                                    "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}})
+        del grouped, per_linear
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -297,9 +344,11 @@ def main() -> int:
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "wall_s": round(wall, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_source,
                      "kernel": f"{dom['type']} {dom['shard']} {dom['N']}x{dom['K']} M={M}", "symbol": dom_symbol,
                      "launch_us": dom["us"], "bytes_per_launch": dom_bytes},
         "shards": rows,
+        "shards_extra_m": extra,
         "gemm": gemm,
         "stack": stack,
     }

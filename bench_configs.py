@@ -156,12 +156,13 @@ def build_stack(torch, gguf_hip, random_shard, dev, layers: int):
 
 
 def time_stack(torch, gguf_hip, dev, lst, M: int) -> float:
-    """ms per step of one pass over the stack's launches at M rows (graph replays, median)."""
-    xs = {K: torch.randn(M, K, device=dev).to(torch.bfloat16) for K in (5120, 17408)}
+    """ms per step of one pass over the stack's launches at M rows (graph replays, median).  Every
+    launch reads an input of its own, as a decoder's linear calls do."""
+    xs = [torch.randn(M, K, device=dev).to(torch.bfloat16) for K, _ in lst]
 
     def f():
-        for K, gl in lst:
-            gguf_hip.mul_mat_grouped(xs[K], gl)
+        for x, (_, gl) in zip(xs, lst):
+            gguf_hip.mul_mat_grouped(x, gl)
     g = _capture(f, torch)
     t = _median_ms(g, torch, 1, reps=2)
     del g

@@ -31,15 +31,16 @@ int check_launch(const char* what) {
   return GQK_OK;
 }
 
-// GEMV wave target when the caller gives none: eight waves per CU of the device current at plan
-// time (2048 on a 256-CU MI355X, also assumed when no device is visible).  A workgroup takes one
-// 64-row tile and up to four waves split its k-range (measured: more waves per workgroup, or
-// more waves than stay resident at once, run slower); shards with too few tiles for the target
-// also split K across workgroups (partials combined in-kernel).
+// GEMV wave target when the caller gives none: eight waves per CU of the plan's device (2048 on a
+// 256-CU MI355X).  A workgroup takes one 64-row tile and up to four waves split its k-range
+// (measured: more waves per workgroup, or more waves than stay resident at once, run slower);
+// shards with too few tiles for the target also split K across workgroups (partials combined
+// in-kernel).
 constexpr int kWavesPerCu = 8;
 constexpr int kGemvWaves = 4;
 
-// CUs of the current device (256 when none is visible: the plan of a host without a GPU)
+// CUs of the current device (256 when none is visible: the plan of a host without a GPU); only
+// asked when the caller of gqk_plan passes cus = 0
 static int current_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -49,7 +50,6 @@ static int current_cus() {
   }
   return cus;
 }
-int64_t default_target_waves() { return (int64_t)kWavesPerCu * current_cus(); }
 
 // bytes of the fp32 split-K partials: [tile][split][64 rows][m_max tokens]
 int64_t gqk_partial_bytes(int64_t tiles, int64_t split, int64_t m_max) { return tiles * split * 64 * m_max * 4; }
@@ -189,9 +189,11 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
   return repack_common(W, w_row_stride, ggml_type, n, K, (void*)tiles, false, stream);
 }
 
-int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
+int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int cus, int32_t* desc,
              int64_t desc_capacity, gqk_plan_info* info) {
   if (!shards || nshards <= 0 || !info) return fail(GQK_ERR_ARG, "plan: no shards / info");
+  if (cus < 0) return fail(GQK_ERR_ARG, "plan: cus=%d", cus);
+  if (cus == 0) cus = current_cus();
   if (K <= 0 || K % 256 != 0) return fail(GQK_ERR_SHAPE, "plan: K=%lld is not a positive multiple of 256", (long long)K);
   if (M <= 0) return fail(GQK_ERR_SHAPE, "plan: M=%d", M);
   const int64_t nb = K / 256;
@@ -252,9 +254,6 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
-#ifdef GQK_GEMV_MIN_G
-    pi.g = std::max(pi.g, GQK_GEMV_MIN_G);
-#endif
     pi.m_max = 4 * pi.g;
     // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
     // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
@@ -262,7 +261,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
     // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
     // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
-    int64_t target = target_wgs > 0 ? target_wgs : default_target_waves();
+    int64_t target = target_wgs > 0 ? target_wgs : (int64_t)kWavesPerCu * cus;
     // Up to four rows (one token group), when every wave can hold exactly one record (k-range a
     // multiple of four super-blocks, at most GQK_SPLIT_MAX workgroups per tile): one record per
     // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances
@@ -348,7 +347,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     if (pi.bm == 256 && (M <= 384 || (M <= 768 && nb <= 32))) {
       int64_t groups = 0;
       for (int i = 0; i < nshards; ++i) groups += ((shards[i].n + 63) / 64 + 3) / 4;
-      if (groups * ((M + 255) / 256) * 4 < current_cus()) pi.bm = 128;
+      if (groups * ((M + 255) / 256) * 4 < cus) pi.bm = 128;
     }
     pi.m_max = 1 << 30;
     pi.split = 1;
@@ -433,7 +432,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     return fail(GQK_ERR_SHAPE, "linear: x must be 16-byte aligned with a row stride that is a multiple of 8");
   if (info->form == GQK_FORM_GEMV) {
     if (M > info->m_max) return fail(GQK_ERR_FORM, "linear: M=%d above the GEMV plan's %d rows", M, info->m_max);
-    if (info->g != 1 && info->g != 2 && info->g != 4 && info->g != 8) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
+    if (info->g != 1 && info->g != 2 && info->g != 4) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
     int* counters = nullptr;
     float* partials = nullptr;
     if (info->workspace_bytes > 0) {

@@ -428,8 +428,10 @@ __device__ __forceinline__ void stage_load(const uint16_t* __restrict__ x, int64
   }
 }
 
+// Tokens t >= M hold clamped copies of row M - 1 (stage_load): their slots and sums reach only
+// outputs of those tokens, which are never stored, so nothing is masked here.
 template <int MPAD, int FAM, bool XG>
-__device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const uint4 (&v)[(8 * MPAD + 63) / 64][4]) {
+__device__ __forceinline__ void stage_store(uint8_t* wl, int lane, const uint4 (&v)[(8 * MPAD + 63) / 64][4]) {
   constexpr int NI = (8 * MPAD + 63) / 64;
   uint2* xs = (uint2*)wl;
   float* xsum16 = (float*)(wl + WaveX<MPAD>::X);
@@ -446,25 +448,13 @@ __device__ __forceinline__ void stage_store(uint8_t* wl, int M, int lane, const 
       for (int j = 0; j < 8; ++j) a += bf2f(w[j] & 0xFFFF) + bf2f(w[j] >> 16);
 #pragma unroll
       for (int j = 8; j < 16; ++j) b += bf2f(w[j] & 0xFFFF) + bf2f(w[j] >> 16);
-      const bool live = t < M;
 #pragma unroll
-      for (int m = 0; m < 8; ++m) xs[x_slot<MPAD, XG>(s32 * 8 + m, t)] = live ? o[m] : make_uint2(0, 0);
-      xsum16[(2 * s32) * MPAD + t] = live ? a : 0.f;
-      xsum16[(2 * s32 + 1) * MPAD + t] = live ? b : 0.f;
-      xsum32[s32 * MPAD + t] = live ? a + b : 0.f;
+      for (int m = 0; m < 8; ++m) xs[x_slot<MPAD, XG>(s32 * 8 + m, t)] = o[m];
+      xsum16[(2 * s32) * MPAD + t] = a;
+      xsum16[(2 * s32 + 1) * MPAD + t] = b;
+      xsum32[s32 * MPAD + t] = a + b;
     }
   }
-}
-
-// Records held per wave: two (one decoded while the next is in flight).  A third costs a wave
-// per SIMD of occupancy, and measured slower for every format: more waves hide more latency.
-template <int G, int T>
-__host__ __device__ constexpr int gemv_depth() {
-#ifdef GQK_GEMV_DEPTH
-  return GQK_GEMV_DEPTH;
-#else
-  return 2;
-#endif
 }
 
 template <int G, int T, class P>
@@ -548,53 +538,45 @@ __device__ __forceinline__ void gemv_wave(const uint8_t* __restrict__ tbase, con
     D r;
     stage_load<MPAD>(x, ldx, M, kw0, lane, xs);
     r.load(tbase + (int64_t)kw0 * (64 * D::REC), lane);
-    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, M, lane, xs);
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, lane, xs);
     process(r);
     return;
   }
   if constexpr (!ONE) gemv_pipeline<G, T>(tbase, x, ldx, M, kw0, kw1, wl, lane, process);
 }
 
-// The register pipeline of a wave with two or more records, DEPTH super-blocks deep: while
-// record kb is decoded, the records (and the x slices) of kb+1 .. kb+DEPTH-1 are in flight.  Each
-// step issues x(kb+DEPTH) and then the record kb+DEPTH, so every wait (x of a step before its LDS
-// write, the record before its decode) covers exactly the loads it needs under the in-order
-// vmcnt count.  Every load is unconditional (addresses clamped to the wave's last super-block, so
-// the tail re-reads it from L2) and the buffers rotate by code position, never by copy.
+// The register pipeline of a wave with two or more records, two super-blocks deep: while record
+// kb is decoded, the record (and the x slice) of kb+1 is in flight.  Each step issues x(kb+2) and
+// then the record kb+2, so every wait (x of a step before its LDS write, the record before its
+// decode) covers exactly the loads it needs under the in-order vmcnt count.  Every load is
+// unconditional (addresses clamped to the wave's last super-block, so the tail re-reads it from
+// L2) and the buffers rotate by code position, never by copy.  (A third record in flight costs a
+// wave per SIMD of occupancy and measured slower for every format.)
 template <int G, int T, class P>
 __device__ __forceinline__ void gemv_pipeline(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x,
                                               int64_t ldx, int M, int kw0, int kw1, uint8_t* wl, int lane,
                                               const P& process) {
   typedef Dec<T> D;
   constexpr int MPAD = 4 * G, NI = (8 * MPAD + 63) / 64;
-  constexpr int DEPTH = gemv_depth<G, T>();
   const int last = kw1 - 1;
   auto rec = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
-  uint4 x0[NI][4], x1[NI][4], x2[NI][4];
-  D r0, r1, r2;
+  uint4 x0[NI][4], x1[NI][4];
+  D r0, r1;
   stage_load<MPAD>(x, ldx, M, kw0, lane, x0);
   r0.load(rec(kw0), lane);
   stage_load<MPAD>(x, ldx, M, min(kw0 + 1, last), lane, x1);
   r1.load(rec(kw0 + 1), lane);
-  if constexpr (DEPTH == 3) {
-    stage_load<MPAD>(x, ldx, M, min(kw0 + 2, last), lane, x2);
-    r2.load(rec(kw0 + 2), lane);
-  }
   auto step = [&](D& r, uint4 (&xv)[NI][4], int kb) {
-    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, M, lane, xv);
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, lane, xv);
     process(r);
-    stage_load<MPAD>(x, ldx, M, min(kb + DEPTH, last), lane, xv);
-    r.load(rec(kb + DEPTH), lane);
+    stage_load<MPAD>(x, ldx, M, min(kb + 2, last), lane, xv);
+    r.load(rec(kb + 2), lane);
   };
-  for (int kb = kw0;; kb += DEPTH) {
+  for (int kb = kw0;; kb += 2) {
     step(r0, x0, kb);
     if (kb + 1 > last) break;
     step(r1, x1, kb + 1);
-    if constexpr (DEPTH == 3) {
-      if (kb + 2 > last) break;
-      step(r2, x2, kb + 2);
-    }
-    if (kb + DEPTH > last) break;
+    if (kb + 2 > last) break;
   }
 }
 
@@ -773,11 +755,7 @@ __device__ __forceinline__ void gemv_wave_w16(const uint8_t* __restrict__ tbase,
 // Q6_K at G = 4 measured 0-8% faster on gate_up and 2-4% slower on down at three.
 template <int G, int ONLY>
 constexpr int gemv_waves() {
-#ifdef GQK_GEMV_WAVES
-  return GQK_GEMV_WAVES;
-#else
   return (G == 2 && ONLY == GQK_Q6_K) ? 3 : 1;
-#endif
 }
 
 template <int G, int ONLY, bool ONE>

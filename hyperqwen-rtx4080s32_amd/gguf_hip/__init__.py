@@ -5,7 +5,7 @@
     from gguf_hip import GGUFFile, load_grouped_layers      # GGUF v3 files -> grouped layers
 """
 from .ops import (  # noqa: F401
-    GGUF_TYPES, TYPE_NAMES, GroupedLayer, dequantize, dequantize_tiles, fused_mul_mat_gguf,
+    GGUF_TYPES, TYPE_NAMES, GroupedLayer, dequantize, dequantize_tiles, drop_cached_layers, fused_mul_mat_gguf,
     fused_mul_mat_gguf_grouped, ggml_dequantize, grouped_layer_from_packed, mul_mat_grouped, pack_layer, plan,
     prepare_grouped_layer,
     quant_shape, repack_tiles, tiles_bytes, type_info, type_planes, unrepack_tiles,

@@ -85,7 +85,7 @@ def _load() -> ctypes.CDLL:
         "gqk_tiles_bytes": (i64, [i32, i64, i64]),
         "gqk_repack": (i32, [vp, i64, i32, i64, i64, vp, vp]),
         "gqk_unrepack": (i32, [vp, i32, i64, i64, vp, i64, vp]),
-        "gqk_plan": (i32, [ctypes.POINTER(GqkShard), i32, i64, i32, i32, ctypes.POINTER(ctypes.c_int32), i64,
+        "gqk_plan": (i32, [ctypes.POINTER(GqkShard), i32, i64, i32, i32, i32, ctypes.POINTER(ctypes.c_int32), i64,
                            ctypes.POINTER(GqkPlanInfo)]),
         "gqk_linear_workspace_bytes": (i64, [ctypes.POINTER(GqkPlanInfo), i32]),
         "gqk_workspace_bytes_max": (i64, []),

@@ -17,7 +17,12 @@ at the level of what a caller can observe:
   view's offset, shape, strides, type and the base's version counter - the reference keys its
   layer caches by the layer's own metadata for the same reason (a freed layer's table must not
   serve another, ``gguf-plugin/gluon/tiles_grouped.py:271-275``).  Later calls allocate only the
-  output: no repack, no host-to-device copy, capturable in a HIP graph.
+  output: no repack, no host-to-device copy, capturable in a HIP graph.  The reference decodes the
+  raw rows in place; here the cache holds a tile copy beside them (the weight's size again in
+  HBM, freed by ``ops.drop_cached_layers``), and a first call made under graph capture raises.
+  The split-K / stream-K launches share the device's workspace (``ops.device_workspace``), so
+  calls that may overlap in time on different streams need a workspace of their own
+  (``ops.mul_mat_grouped(..., workspace=)``).
 """
 from __future__ import annotations
 

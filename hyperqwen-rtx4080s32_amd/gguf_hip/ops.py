@@ -173,13 +173,15 @@ def dequantize_tiles(tiles: torch.Tensor, n_out: int, K: int, weight_type: int, 
 # ----------------------------------------------------------------------------------------------
 # grouped layers
 
-def plan(shards: list[tuple[int, int, int]], K: int, M: int, target_wgs: int = 0) -> tuple[GqkPlanInfo, torch.Tensor]:
-    """Host plan of a grouped launch: shards = [(type, n, byte offset)] -> (info, int32 table on CPU)."""
+def plan(shards: list[tuple[int, int, int]], K: int, M: int, target_wgs: int = 0,
+         cus: int = 0) -> tuple[GqkPlanInfo, torch.Tensor]:
+    """Host plan of a grouped launch: shards = [(type, n, byte offset)] -> (info, int32 table on CPU).
+    cus: compute units of the target device (0: the current device's, as the HIP runtime reports)."""
     arr = (GqkShard * len(shards))(*[GqkShard(int(t), 0, int(n), int(o)) for t, n, o in shards])
     info = GqkPlanInfo()
-    check(lib.gqk_plan(arr, len(shards), K, M, target_wgs, None, 0, ctypes.byref(info)), "plan")
+    check(lib.gqk_plan(arr, len(shards), K, M, target_wgs, cus, None, 0, ctypes.byref(info)), "plan")
     desc = torch.empty(info.n_desc * 16, dtype=torch.int32)
-    check(lib.gqk_plan(arr, len(shards), K, M, target_wgs,
+    check(lib.gqk_plan(arr, len(shards), K, M, target_wgs, cus,
                        ctypes.cast(desc.data_ptr(), ctypes.POINTER(ctypes.c_int32)), desc.numel(), ctypes.byref(info)),
           "plan")
     return info, desc
@@ -371,6 +373,9 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
 
 
 _CACHE_ATTR = "_gguf_hip_layers"
+# views of one base tensor whose layers the cache keeps (a merged qkv / gate_up parameter has 2-3
+# shard views); beyond it the least recently used entry is dropped
+CACHE_MAX_VIEWS = 8
 
 
 def cached_layer(weight: torch.Tensor, weight_type: int, n_out: int, kind: str = "rows") -> GroupedLayer:
@@ -380,7 +385,13 @@ def cached_layer(weight: torch.Tensor, weight_type: int, n_out: int, kind: str =
     and a freed weight's entry can never serve another (the reference keys its caches by the
     layer's own metadata for that reason, gguf-plugin/gluon/tiles_grouped.py:271-275).  The key is
     the view's offset, shape, strides, type and rows, and the entry is rebuilt when the base's
-    version counter shows an in-place write.  Later calls allocate nothing and copy nothing."""
+    version counter shows an in-place write.  Later calls allocate nothing and copy nothing.
+
+    Memory: for raw rows the entry holds a repacked copy of the weight (its own size again in
+    HBM) beside the raw rows, which stay with their owner; ``drop_cached_layers(weight)`` frees
+    it, and at most ``CACHE_MAX_VIEWS`` views of one base tensor are kept (least recently used
+    dropped).  The first call on a weight repacks and plans (allocations, a host-to-device copy of
+    the plans), so it raises under HIP graph capture: make it once eagerly before capturing."""
     base = weight._base if weight._base is not None else weight
     key = (kind, weight.storage_offset(), tuple(weight.shape), tuple(weight.stride()), int(weight_type), int(n_out),
            str(weight.device))
@@ -390,7 +401,13 @@ def cached_layer(weight: torch.Tensor, weight_type: int, n_out: int, kind: str =
         setattr(base, _CACHE_ATTR, cache)
     hit = cache.get(key)
     if hit is not None and hit[0] == base._version:
+        cache[key] = cache.pop(key)          # most recently used last
         return hit[1]
+    if weight.is_cuda and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            "gguf_hip: the first call on a GGUF weight repacks it into the tile layout and uploads its launch "
+            "plans (device allocations and a host-to-device copy), which a HIP graph capture cannot record; "
+            "call it once eagerly before capturing (later calls allocate only the output)")
     if kind == "rows":
         gl = pack_layer([weight], [n_out], [weight_type])
     elif kind == "tiles":
@@ -402,8 +419,23 @@ def cached_layer(weight: torch.Tensor, weight_type: int, n_out: int, kind: str =
         gl = grouped_layer_from_packed(flat, [n_out], [weight_type], per_row // rec * 256)
     else:
         raise ValueError(f"cached_layer: kind {kind!r}")
+    cache.pop(key, None)
     cache[key] = (base._version, gl)
+    while len(cache) > CACHE_MAX_VIEWS:
+        cache.pop(next(iter(cache)))
     return gl
+
+
+def drop_cached_layers(weight: torch.Tensor) -> int:
+    """Frees the layers ``cached_layer`` keeps for every view of weight's base tensor (their tile
+    copies and plans); returns how many were dropped.  A later call on the weight rebuilds its entry."""
+    base = weight._base if weight._base is not None else weight
+    cache = getattr(base, _CACHE_ATTR, None)
+    if not cache:
+        return 0
+    n = len(cache)
+    cache.clear()
+    return n
 
 
 def fused_mul_mat_gguf(x: torch.Tensor, qweight: torch.Tensor, qweight_type: int) -> torch.Tensor:

@@ -28,8 +28,8 @@ extern "C" {
 #define GQK_ERR_HIP (-4)   /* HIP runtime error at launch */
 #define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
 
-#define GQK_FORM_GEMV 1 /* M <= 16 (<= 8 with an IQ shard): in-register decode GEMV (MFMA 4x4x4 per scale group) */
-#define GQK_FORM_GEMM 2 /* above: LDS-dequant bf16 MFMA GEMM (any M) */
+#define GQK_FORM_GEMV 1 /* M <= 16, every type: in-register decode GEMV (MFMA per scale group) */
+#define GQK_FORM_GEMM 2 /* M > 16: LDS-dequant bf16 MFMA GEMM (any M) */
 
 #define GQK_CTR_BYTES 262144 /* the arrival-counter region at the start of every workspace */
 
@@ -100,16 +100,17 @@ int gqk_repack(const void* W, int64_t w_row_stride, int ggml_type, int64_t n, in
  * (gguf-plugin/gluon/tiles.py:56-67). */
 int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W, int64_t w_row_stride, void* stream);
 
-/* Host-only: the launch plan of a grouped layer (shards packed back to back, all of K columns)
- * for batch rows M: fills *info and, if desc is not NULL and desc_capacity (int32 words) is
- * enough, the descriptor table (16 int32 per row) to upload to the device.  target_wgs > 0
- * overrides the GEMV heuristic's target of resident waves (0 = default: eight per CU of the
- * device current at the call, 256 CUs assumed when none is visible), from which the waves per
- * workgroup and the split-K factor follow.  GEMM plans (M > 16) take their tile form from M and,
- * at 129..384 rows, from the layer's size against the same device's CU count.  Replaces
- * prepare_grouped_layer / descriptors / grouped_split_for
+/* Host code (no launch, no allocation): the launch plan of a grouped layer (shards packed back to
+ * back, all of K columns) for batch rows M: fills *info and, if desc is not NULL and
+ * desc_capacity (int32 words) is enough, the descriptor table (16 int32 per row) to upload to
+ * the device.  cus: compute units of the device the plan is for (256 on MI355X); 0 asks the HIP
+ * runtime for the current device's count (initialising the runtime; 256 when no device is
+ * visible).  target_wgs > 0 overrides the GEMV heuristic's target of resident waves (0 = eight per
+ * CU), from which the waves per workgroup and the split-K factor follow.  GEMM plans (M > 16)
+ * take their tile form from M and, at 129..384 rows (129..768 for K <= 8192), from the layer's
+ * size against the CU count.  Replaces prepare_grouped_layer / descriptors / grouped_split_for
  * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
-int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int32_t* desc,
+int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_wgs, int cus, int32_t* desc,
              int64_t desc_capacity, gqk_plan_info* info);
 
 /* Device workspace bytes gqk_linear needs for this plan at M batch rows (0: none; < 0: error).
@@ -142,8 +143,11 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
  * in the reference.  The split-K / stream-K counters and partials live in a file-scope device
  * array of GQK_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends; its address is taken
  * once per device on the first call, which also clears its counters with a fill kernel on
- * `stream`).  Allocates nothing.  A plan that needs more workspace at this M (GEMM plans above 64
- * rows on large layers can) is refused with GQK_ERR_SHAPE.  Every call on one GPU shares that
+ * `stream`).  Allocates nothing.  A plan that needs more workspace at this M is refused with
+ * GQK_ERR_SHAPE: GEMM plans above 64 rows on large layers, and GEMV plans whose split-K partials
+ * exceed the 32 MiB (those are 64 rows x m_max tokens x 4 bytes per partial slot: at most 8,192
+ * slots at m_max = 16, 32,768 at m_max = 4; e.g. a layer of 2,374 tiles at K = 16384 split 16 ways
+ * at M <= 4 needs ~39 MB).  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (other streams, other threads) race. */
 #define GQK_NOALLOC_SCRATCH_BYTES (GQK_CTR_BYTES + 33554432)
 int gqk_linear_noalloc(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x,

@@ -13,6 +13,32 @@ from oracle import ggml_ref as G
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
+def _plan(*args, **kw):
+    """ops.plan on a pinned 256-CU device (MI355X), so the CPU tests do not depend on a visible GPU."""
+    from gguf_hip import ops
+
+    return ops.plan(*args, cus=kw.pop("cus", 256), **kw)
+
+
+def test_plan_takes_the_cu_count():
+    """The CU count is a plan input: the default wave target is eight per CU, and the 128 x 128
+    GEMM form's choice compares a layer's 256-row groups against it; a negative count is refused."""
+    from gguf_hip import _lib
+
+    # gate_up at M = 8 (544 tiles of 20 records): 256 CUs -> 2048 waves, 4 per tile, 512 slots:
+    # 512 whole tiles and the last 32 split min(20 / 4, 512 / 2 / 32) = 5 ways; 128 CUs -> 1024
+    # waves, 2 per tile, 512 slots of 2-wave workgroups: the last 32 split min(20 / 2, 8) = 8 ways
+    info = _plan([(12, 34816, 0)], 5120, 8)[0]
+    assert (info.nw, info.n_desc) == (4, 512 + 32 * 5)
+    info = _plan([(12, 34816, 0)], 5120, 8, cus=128)[0]
+    assert (info.nw, info.n_desc) == (2, 512 + 32 * 8)
+    # o_proj 5120 x 5120 at M = 200: 20 groups of 256 rows * 4 < 256 CUs -> 128 x 128 tiles; not on 64 CUs
+    assert _plan([(12, 5120, 0)], 5120, 200)[0].bm == 128
+    assert _plan([(12, 5120, 0)], 5120, 200, cus=64)[0].bm == 256
+    with pytest.raises(ValueError):
+        _plan([(12, 5120, 0)], 5120, 8, cus=-1)
+
+
 def test_exports_every_declared_symbol():
     from gguf_hip import _lib
 
@@ -58,11 +84,11 @@ def test_unsupported_type_and_bad_shapes():
     assert _lib.lib.gqk_tiles_bytes(12, 10, 300) == _lib.GQK_ERR_SHAPE
     assert _lib.lib.gqk_tiles_bytes(12, 70, 512) == 128 * 2 * 144
     with pytest.raises(ValueError):
-        ops.plan([(12, 64, 0), (21, 64, 12345)], 512, 1)  # shards not back to back
+        _plan([(12, 64, 0), (21, 64, 12345)], 512, 1)  # shards not back to back
     with pytest.raises(ValueError):
-        ops.plan([(12, 64, 0)], 500, 1)                  # K not a multiple of 256
+        _plan([(12, 64, 0)], 500, 1)                  # K not a multiple of 256
     with pytest.raises(NotImplementedError):
-        ops.plan([(12, 64, 0), (16, 64, 64 * 2 * 144)], 512, 1)
+        _plan([(12, 64, 0), (16, 64, 64 * 2 * 144)], 512, 1)
     with pytest.raises(ValueError):
         ops.quant_shape(12, 4, 145)
 
@@ -107,7 +133,7 @@ def test_plan_gemv_balanced_split_partition():
     from gguf_hip import _lib, ops
 
     for target in (1, 16, 97, 1024, 4096, 0):
-        info, desc = ops.plan([(21, 6144, 0)], 20 * 256, 1, target)
+        info, desc = _plan([(21, 6144, 0)], 20 * 256, 1, target)
         ncs = _check_gemv_rows([(21, 6144, 0)], 20 * 256, info, desc)
         S, nw = info.split, info.nw
         assert info.form == 1 and info.g == 1 and info.m_max == 4
@@ -117,10 +143,10 @@ def test_plan_gemv_balanced_split_partition():
         assert set(ncs.values()) == {S}                     # 96 tiles: one round or whole rounds, no tail
         # the counter region: the fixed GQK_CTR_BYTES of every plan
         assert info.ctr_bytes == _lib.GQK_CTR_BYTES
-    assert ops.plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
-    info = ops.plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
+    assert _plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
+    info = _plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
     assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
-    info = ops.plan([(21, 6144, 0)], 20 * 256, 8, 0)[0]
+    info = _plan([(21, 6144, 0)], 20 * 256, 8, 0)[0]
     assert (info.nw, info.split) == (4, 5)                  # default target 2048 waves: 22 per tile
 
 
@@ -131,53 +157,53 @@ def test_plan_gemv_tail_tiles_split():
 
     # gate_up 34816 x 5120 at the default target: 544 tiles, 512 slots of 4 waves -> 512 whole
     # tiles, the last 32 split 5 ways (>= one record per wave; up to 8 would fit half the slots)
-    info, desc = ops.plan([(12, 34816, 0)], 5120, 8, 0)
+    info, desc = _plan([(12, 34816, 0)], 5120, 8, 0)
     ncs = _check_gemv_rows([(12, 34816, 0)], 5120, info, desc)
     order = [ncs[k] for k in sorted(ncs, key=lambda k: k[1])]
     assert order == [1] * 512 + [5] * 32 and info.n_desc == 512 + 160 and info.nw == 4
     # a full last round (no remainder) and a long one (> half the slots) stay whole
-    info, desc = ops.plan([(12, 32768, 0)], 5120, 8, 0)
+    info, desc = _plan([(12, 32768, 0)], 5120, 8, 0)
     assert set(_check_gemv_rows([(12, 32768, 0)], 5120, info, desc).values()) == {1} and info.workspace_bytes == 0
-    info, desc = ops.plan([(12, 64 * 13, 0)], 16 * 256, 1, 16)     # 13 tiles, 8 slots of 2 waves
+    info, desc = _plan([(12, 64 * 13, 0)], 16 * 256, 1, 16)     # 13 tiles, 8 slots of 2 waves
     assert info.nw == 2 and set(_check_gemv_rows([(12, 64 * 13, 0)], 16 * 256, info, desc).values()) == {1}
     # 800 tiles at the default target: 3 waves each, 682 slots, the last 118 tiles split 2 ways
-    info, desc = ops.plan([(12, 64 * 800, 0)], 5120, 8, 0)
+    info, desc = _plan([(12, 64 * 800, 0)], 5120, 8, 0)
     ncs = _check_gemv_rows([(12, 64 * 800, 0)], 5120, info, desc)
     assert info.nw == 3 and sorted(ncs.values()) == [1] * 682 + [2] * 118
     # the tail spans shards: 34816 rows after a 1024-row shard of the same type (560 tiles, 48 split)
     offq = ops.tiles_bytes(14, 1024, 5120)
-    info, desc = ops.plan([(14, 1024, 0), (14, 34816, offq)], 5120, 8, 0)
+    info, desc = _plan([(14, 1024, 0), (14, 34816, offq)], 5120, 8, 0)
     ncs = _check_gemv_rows([(14, 1024, 0), (14, 34816, offq)], 5120, info, desc)
     assert sum(1 for v in ncs.values() if v > 1) == 48 and info.split == min(5, 256 // 48)
     off = ops.tiles_bytes(12, 1024, 5120)
     # up to four rows the same layer takes one record per wave: every tile split 5 ways x 4 waves
-    info, desc = ops.plan([(12, 1024, 0), (14, 34816, off)], 5120, 1, 0)
+    info, desc = _plan([(12, 1024, 0), (14, 34816, off)], 5120, 1, 0)
     ncs = _check_gemv_rows([(12, 1024, 0), (14, 34816, off)], 5120, info, desc)
     assert set(ncs.values()) == {5} and info.n_desc == 560 * 5 and info.nw == 4 and info.bm == 1
     # ... unless the k-range does not split into single records (down: 68 super-blocks)
-    assert ops.plan([(12, 5120, 0)], 17408, 1, 0)[0].bm == 0
+    assert _plan([(12, 5120, 0)], 17408, 1, 0)[0].bm == 0
     # a mixed-type layer keeps one record per wave up to eight rows (its streaming kernel is bound
     # by its costliest format's registers); a single type streams at eight, and nothing does at 16
     mixed = [(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))]
     for M, bm in ((1, 1), (8, 1), (16, 0)):
-        info, desc = ops.plan(mixed, 5120, M, 0)
+        info, desc = _plan(mixed, 5120, M, 0)
         assert info.bm == bm and info.types_mask == 0, M
         if bm:
             assert set(_check_gemv_rows(mixed, 5120, info, desc).values()) == {5} and info.n_desc == 192 * 5
-    assert ops.plan([(12, 7168, 0)], 5120, 8, 0)[0].bm == 1 and ops.plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
+    assert _plan([(12, 7168, 0)], 5120, 8, 0)[0].bm == 1 and _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
     # one round of split tiles with >= 2 records a wave fills the 512 slots exactly: down 5120 x
     # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; qkv (1 record a wave) keeps 5 each
-    info, desc = ops.plan([(12, 5120, 0)], 17408, 8, 0)
+    info, desc = _plan([(12, 5120, 0)], 17408, 8, 0)
     ncs = _check_gemv_rows([(12, 5120, 0)], 17408, info, desc)
     assert info.n_desc == 512 and sorted(ncs.values()) == [6] * 48 + [7] * 32 and info.split == 7
-    info, desc = ops.plan([(12, 7168, 0)], 5120, 8, 0)
+    info, desc = _plan([(12, 7168, 0)], 5120, 8, 0)
     assert set(_check_gemv_rows([(12, 7168, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 560
     # the GEMV's bm field flags plans whose waves all stream exactly one record (qkv, o_proj at
     # K = 5120: 20 records = 5 workgroups x 4 waves); the pipeline-free kernel serves them
-    assert info.bm == 1 and ops.plan([(12, 5120, 0)], 5120, 1, 0)[0].bm == 1
-    assert ops.plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0 and ops.plan([(12, 5120, 0)], 17408, 8, 0)[0].bm == 0
+    assert info.bm == 1 and _plan([(12, 5120, 0)], 5120, 1, 0)[0].bm == 1
+    assert _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0 and _plan([(12, 5120, 0)], 17408, 8, 0)[0].bm == 0
     # small targets: 10 tiles on 8 slots of 2 waves... (target 16) -> the last 2 tiles split
-    info, desc = ops.plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
+    info, desc = _plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
     ncs = _check_gemv_rows([(12, 64 * 9 + 17, 0)], 16 * 256, info, desc)
     assert info.nw == 2 and sorted(ncs.values()) == [1] * 8 + [2, 2]
 
@@ -191,7 +217,7 @@ def test_plan_all_split_rows_interleaved_by_xcd():
 
     for shards, K, M in (([(12, 5120, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 7168, 0)], 5120, 1),
                          ([(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))], 5120, 8)):
-        info, desc = ops.plan(shards, K, M)
+        info, desc = _plan(shards, K, M)
         d = _rows(desc)
         assert all(r[12] > 1 for r in d), (shards, K, M)
         _check_gemv_rows([(wt, n, o) for wt, n, o in shards], K, info, desc)
@@ -201,7 +227,7 @@ def test_plan_all_split_rows_interleaved_by_xcd():
             work[i % 8] += int(r[6]) - int(r[5])
         assert all(len(v) == 1 for v in residues.values()), (shards, K, M)
         assert max(work) - min(work) <= K // 256, (shards, K, M, work)
-    info, desc = ops.plan([(12, 34816, 0)], 5120, 8)            # 512 whole tiles + a split tail
+    info, desc = _plan([(12, 34816, 0)], 5120, 8)            # 512 whole tiles + a split tail
     tiles = [int(r[3]) for r in _rows(desc)]
     assert tiles[:512] == list(range(512)) and tiles == sorted(tiles)
 
@@ -226,7 +252,7 @@ def test_plan_random_layers_stay_in_bounds():
             off += ops.tiles_bytes(wt, n, K)
         M = int(rng.choice([rng.integers(1, 17), rng.integers(17, 601)]))
         target = int(rng.choice([0, 0, 1, 16, int(rng.integers(2, 5000))]))
-        info, desc = ops.plan(shards, K, M, target)
+        info, desc = _plan(shards, K, M, target)
         d = _rows(desc)
         nb, n_total = K // 256, sum(n for _, n, _ in shards)
         tiles_of = {o: ((n + 63) // 64, n, wt) for wt, n, o in shards}
@@ -271,17 +297,17 @@ def test_plan_descriptor_rows_mixed_layer():
 
     K = 3 * 256
     off2 = ops.tiles_bytes(21, 70, K)
-    info, desc = ops.plan([(21, 70, 0), (12, 300, off2)], K, 8, 4)
+    info, desc = _plan([(21, 70, 0), (12, 300, off2)], K, 8, 4)
     d = _rows(desc)
     assert info.types_mask == 0 and info.n_total == 370 and info.g == 2
     assert info.split == 1 and info.workspace_bytes == 0
     # one counter region for every plan of every layer, so one workspace serves every layer and M
     for shards, k in (([(21, 70, 0), (12, 300, off2)], K), ([(12, 70000, 0)], 512), ([(12, 64 * 65536, 0)], 256)):
-        regions = {ops.plan(shards, k, m, t)[0].ctr_bytes for m in (1, 8, 16, 17, 100, 2048) for t in (0, 1, 4096)}
+        regions = {_plan(shards, k, m, t)[0].ctr_bytes for m in (1, 8, 16, 17, 100, 2048) for t in (0, 1, 4096)}
         assert regions == {_lib.GQK_CTR_BYTES}
     # a layer with more tiles than the region has counters is refused, not silently overrun
     with pytest.raises(ValueError, match="counter region"):
-        ops.plan([(12, 64 * 65536 + 1, 0)], 256, 8)
+        _plan([(12, 64 * 65536 + 1, 0)], 256, 8)
     # one workgroup per tile: IQ3_S 2 tiles (64 + 6 rows), Q4_K 5 tiles (4 x 64 + 44)
     assert d[:, 0].tolist() == [21, 21, 12, 12, 12, 12, 12]
     assert d[:, 3].tolist() == [0, 1, 0, 1, 2, 3, 4] and d[:, 4].tolist() == [1] * 7
@@ -289,24 +315,24 @@ def test_plan_descriptor_rows_mixed_layer():
     assert d[2, 1] == off2 and d[:, 10].tolist() == [3] * 7 and d[:, 12].tolist() == [1] * 7   # whole tiles
     _check_gemv_rows([(21, 70, 0), (12, 300, off2)], K, info, desc)
     assert info.nw == 1                                     # a target of 4 waves for 7 tiles: one each
-    gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 100)
+    gi, gd = _plan([(21, 70, 0), (12, 300, off2)], K, 100)
     g = _rows(gd)
     assert gi.form == 2 and gi.bm == 128 and g.shape[0] == 1 + 3          # two tiles per row
     assert g[:, 4].tolist() == [2, 2, 2, 1] and g[:, 6].tolist() == [3] * 4
-    gi, gd = ops.plan([(21, 70, 0), (12, 300, off2)], K, 2048)
+    gi, gd = _plan([(21, 70, 0), (12, 300, off2)], K, 2048)
     g = _rows(gd)
     assert gi.form == 2 and gi.bm == 256 and g.shape[0] == 1 + 2          # four tiles per row
     assert g[:, 4].tolist() == [2, 4, 1] and g[:, 9].tolist() == [70, 256, 44]
     assert g[:, 8].tolist() == [0, 70, 326]
-    assert ops.plan([(21, 70, 0), (12, 300, off2)], K, 40)[0].bm == 64
-    assert ops.plan([(21, 70, 0), (12, 300, off2)], K, 20)[0].bm == 32
+    assert _plan([(21, 70, 0), (12, 300, off2)], K, 40)[0].bm == 64
+    assert _plan([(21, 70, 0), (12, 300, off2)], K, 20)[0].bm == 32
 
 
 def test_plan_buckets():
     from gguf_hip import ops
 
     for M, g in ((1, 1), (4, 1), (5, 2), (8, 2), (9, 4), (16, 4)):
-        info, _ = ops.plan([(12, 512, 0)], 512, M)
+        info, _ = _plan([(12, 512, 0)], 512, M)
         assert info.form == 1 and info.g == g and info.m_max == 4 * g
     assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 16) == 2
     assert ops._pick_plan([], 17) == 3 and ops._pick_plan([], 32) == 3 and ops._pick_plan([], 33) == 4
@@ -317,24 +343,24 @@ def test_plan_buckets():
     assert ops._pick_plan([], 769) == 9 and ops._pick_plan([], 8192) == 9
     # every type, the table types (IQ4_NL / IQ4_XS / IQ3_S) included, stays on the GEMV up to 16 rows
     for wt in (20, 23, 21):
-        i9, i16, i17 = (ops.plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17))
+        i9, i16, i17 = (_plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17))
         assert (i9.form, i9.g, i16.form, i16.g, i17.form, i17.bm) == (1, 4, 1, 4, 2, 32)
     off = ops.tiles_bytes(12, 512, 512)
-    assert ops.plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 1
+    assert _plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 1
     for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 128), (384, 128),
                   (512, 128), (768, 128), (769, 256), (2048, 256)):
-        assert ops.plan([(12, 512, 0)], 512, M)[0].bm == bm
+        assert _plan([(12, 512, 0)], 512, M)[0].bm == bm
     # 129..384 rows: 256 x 256 tiles once the 256-row groups times the token blocks reach a quarter
     # of the CUs (256 assumed without a GPU): 34816 rows = 136 groups, 16384 = 64, 16000 = 63,
     # 7168 = 28, 5120 = 20
     for n, M, bm in ((34816, 129, 256), (34816, 384, 256), (7168, 256, 128), (7168, 384, 128),
                      (5120, 384, 128), (16000, 256, 128), (16000, 257, 256), (16384, 129, 256)):
-        assert ops.plan([(12, n, 0)], 512, M)[0].bm == bm, (n, M)
+        assert _plan([(12, n, 0)], 512, M)[0].bm == bm, (n, M)
     # 385..768 rows only for K up to 8192 (32 super-blocks)
     for K, M, bm in ((5120, 512, 128), (8192, 512, 128), (8448, 512, 256), (17408, 448, 256), (17408, 384, 128),
                      (5120, 768, 128), (5120, 769, 256)):
-        assert ops.plan([(12, 5120, 0)], K, M)[0].bm == bm, (K, M)
-    assert ops.plan([(12, 7168, 0)], 5120, 640)[0].bm == 256       # 28 groups x 3 blocks: above the quarter
+        assert _plan([(12, 5120, 0)], K, M)[0].bm == bm, (K, M)
+    assert _plan([(12, 7168, 0)], 5120, 640)[0].bm == 256       # 28 groups x 3 blocks: above the quarter
 
 
 def test_ggml_dequantize_rejects_rows_narrower_than_n():

@@ -21,7 +21,7 @@ def _fake_layer(shards, K, mode):
     for wt, n in shards:
         specs.append((wt, n, off))
         off += ops.tiles_bytes(wt, n, K)
-    plans = [ops.plan(specs, K, m) for m in ops.GEMV_BUCKETS + ops.GEMM_PLAN_M]
+    plans = [ops.plan(specs, K, m, cus=256) for m in ops.GEMV_BUCKETS + ops.GEMM_PLAN_M]
     with mode:
         gl = ops.GroupedLayer(torch.empty(off, dtype=torch.uint8, device="cuda"), [], [n for _, n in shards],
                               [wt for wt, _ in shards], K)

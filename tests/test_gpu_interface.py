@@ -79,6 +79,43 @@ def test_gluon_mul_mat_strided_shards_in_graph(dev):
         I.gluon_mul_mat(_x(1, K, 0, dev), views[0], 16, 130)          # IQ2_XXS: no kernel here
 
 
+def test_gluon_mul_mat_first_call_under_capture_raises(dev):
+    """The raw-row op keeps a tile copy of the weight (made on its first call: device allocations
+    and a plan upload).  A first call inside a HIP graph capture raises a clear error instead of
+    recording them; after one eager call the same capture works, and drop_cached_layers frees the
+    copy (the allocator's count falls back by at least the tiles' bytes)."""
+    from gguf_hip import interface as I
+    from gguf_hip import ops
+
+    rng = np.random.default_rng(33)
+    K, n = 2048, 512
+    raw = G.make_weights(rng, n, K, G.Q4_K)
+    W = torch.from_numpy(raw).to(dev)
+    x = _x(4, K, 7, dev)
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with pytest.raises(RuntimeError, match="capture"):
+        with torch.cuda.graph(g):
+            I.gluon_mul_mat(x, W, G.Q4_K, n)
+    del g
+    torch.cuda.synchronize()
+    assert not getattr(W, "_gguf_hip_layers", None)                   # nothing was cached
+    before = torch.cuda.memory_allocated(dev)
+    eager = I.gluon_mul_mat(x, W, G.Q4_K, n)                          # prepares the tile copy
+    torch.cuda.synchronize()
+    grown = torch.cuda.memory_allocated(dev) - before
+    assert grown >= ops.tiles_bytes(G.Q4_K, n, K)                     # the second copy of the weight
+    g, out = _capture(lambda: I.gluon_mul_mat(x, W, G.Q4_K, n))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    del g, out
+    assert ops.drop_cached_layers(W) == 1
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated(dev) - before <= grown - ops.tiles_bytes(G.Q4_K, n, K)
+
+
 @pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
 def test_gluon_mul_mat_every_type_strided(dev, wt):
     """gluon_mul_mat on a shard view with a row stride wider than its rows and a column offset

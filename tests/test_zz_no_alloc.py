@@ -75,11 +75,22 @@ def test_noalloc_refuses_a_plan_beyond_its_array(dev):
     n, K = 34816, 256
     raw = G.random_blocks(rng, n, K, G.Q4_0)
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_0])
-    M = 4000                                                  # 256 x 256 tiles: stream-K partials well above 32 MiB
+    # the first M (in steps of 256) whose plan needs more workspace than the array on this device
+    # (the stream-K partials depend on the tile count modulo the device's persistent workgroups)
+    from gguf_hip import ops
+
+    M = None
+    for m in range(256, 16385, 256):
+        i = ops._pick_plan(gl.plans, m)
+        info = ops.GqkPlanInfo.from_tuple(gl.plans[i * ops._NPLAN:(i + 1) * ops._NPLAN])
+        if _lib.lib.gqk_linear_workspace_bytes(ctypes.byref(info), m) > _lib.GQK_NOALLOC_SCRATCH_BYTES:
+            M = m
+            break
+    assert M is not None, "no M up to 16384 needs more than the array"
     x = _x(M, K, 5, dev)
     rc, _, info = _call(None, gl, x, False)
     need = _lib.lib.gqk_linear_workspace_bytes(ctypes.byref(info), M)
-    assert info.bm == 256 and need > _lib.GQK_NOALLOC_SCRATCH_BYTES, need
+    assert need > _lib.GQK_NOALLOC_SCRATCH_BYTES, (M, need)
     assert rc == _lib.GQK_ERR_SHAPE and b"no-allocation" in _lib.lib.gqk_last_error()
     # and the same layer at a decode M runs
     rc, y, _ = _call(None, gl, _x(8, K, 6, dev), False)
