@@ -249,11 +249,12 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
   const int64_t ctr_bytes = GQK_CTR_BYTES;
   pi.ctr_bytes = (int32_t)ctr_bytes;
   // The GEMV serves up to 16 rows for every type (with its x operands broadcast from registers
-  // the table types too beat the 32-row GEMM at 16 rows: IQ4_NL / IQ3_S / IQ4_XS 34816 x 5120
-  // 41 / 43 / 42 us against 51 / 56 / 50 us, 5120 x 17408 26-28 us against 39-46 us).
+  // the table types too beat the 32-row GEMM tile at 16 rows: IQ4_NL / IQ3_S / IQ4_XS 34816 x 5120
+  // 41 / 43 / 42 us against 51 / 56 / 50 us, 5120 x 17408 26-28 us against 39-46 us), and the mid
+  // form (g = 8) 17..32 rows with the same descriptor rows, split policy and exchange.
   if (M <= GQK_GEMV_MAX_M) {
     pi.form = GQK_FORM_GEMV;
-    pi.g = M <= 4 ? 1 : M <= 8 ? 2 : 4;
+    pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
     pi.m_max = 4 * pi.g;
     // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
     // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
@@ -328,15 +329,14 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     }
     // a plan whose waves all hold a single record launches the kernel built without the register
     // pipeline (fewer registers: more workgroups resident), flagged in the GEMM-only bm field
-    pi.bm = one_record ? 1 : 0;
+    pi.bm = one_record && pi.g <= 4 ? 1 : 0;
     // workspace: the counter region (one arrival counter per split tile; zero before the first
     // launch, left zero by each launch), then the fp32 partial slots [slot][64 rows][m_max tokens]
     pi.workspace_bytes = slot > 0 ? ctr_bytes + gqk_partial_bytes(slot, 1, pi.m_max) : 0;
   } else {
     pi.form = GQK_FORM_GEMM;
-    // 32 / 64 / 128 tokens x 128 rows per tile up to 128 tokens; 256 x 256 above.  From 17 tokens
-    // on the GEMM outruns the GEMV's 4 x 4 x 4 MFMAs (one decode of each weight for up to 128 tokens).
-    pi.bm = M <= 32 ? 32 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
+    // 64 / 128 tokens x 128 rows per tile up to 128 tokens (one decode of each weight); 256 x 256 above.
+    pi.bm = M <= 64 ? 64 : M <= 128 ? 128 : 256;
     // A layer with few 256-row groups keeps the 128 x 128 form up to 384 rows (768 for K up to
     // 8192) when the 256 x 256 form would have fewer tiles than a quarter of the CUs (one
     // workgroup each): its stream-K would leave most CUs idle and pad the last token block.
@@ -432,7 +432,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
     return fail(GQK_ERR_SHAPE, "linear: x must be 16-byte aligned with a row stride that is a multiple of 8");
   if (info->form == GQK_FORM_GEMV) {
     if (M > info->m_max) return fail(GQK_ERR_FORM, "linear: M=%d above the GEMV plan's %d rows", M, info->m_max);
-    if (info->g != 1 && info->g != 2 && info->g != 4) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
+    if (info->g != 1 && info->g != 2 && info->g != 4 && info->g != 8) return fail(GQK_ERR_FORM, "linear: g=%d", info->g);
     int* counters = nullptr;
     float* partials = nullptr;
     if (info->workspace_bytes > 0) {

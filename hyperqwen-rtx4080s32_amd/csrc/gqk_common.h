@@ -129,9 +129,7 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 // device serves all layers and batch sizes: no plan's fp32 partials overlap another's counters.
 #define GQK_CTR_BYTES 262144   // (mirrored in include/gguf_hip.h)
 #define GQK_CTR_WORDS (GQK_CTR_BYTES / 4)
-#ifndef GQK_GEMV_MAX_M
-#define GQK_GEMV_MAX_M 16   // batch rows served by the GEMV form (every type); the GEMM above
-#endif
+#define GQK_GEMV_MAX_M 32   // batch rows of the streaming forms (GEMV up to 16, mid form 17..32); GEMM above
 #define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
 enum {
   D_TYPE = 0,     // GGML type of the row's shard
@@ -156,5 +154,7 @@ void gqk_set_last_error(const char* msg);
 #endif
 
 // forms of a grouped launch
-#define GQK_FORM_GEMV 1   // M <= 16: in-register decode, MFMA 4x4x4 per sub-block, fp32 epilogue
-#define GQK_FORM_GEMM 2   // M > 16: tile decoded to bf16 in LDS, MFMA 32x32x16
+#define GQK_FORM_GEMV 1   // M <= 32, descriptor rows of (tile, k-range): M <= 16 the GEMV (in-register
+                          // decode, MFMA per scale group, fp32 epilogue); 17..32 the mid form (g = 8:
+                          // weights decoded to bf16 in registers, MFMA 32x32x16)
+#define GQK_FORM_GEMM 2   // M > 32: tile decoded to bf16 in LDS, MFMA 32x32x16

@@ -1,4 +1,5 @@
-// gqk_gemm.hip - the grouped dequant-GEMM (batch rows M > 16, the prefill regime).
+// gqk_gemm.hip - the grouped dequant-GEMM (batch rows M > 32, the prefill regime) and the mid
+// form (17..32 rows) that shares its decoders.
 //
 // Replaces the reference's prefill paths: the wide int8 forms of the grouped kernel and, for
 // Q4_K / Q5_K, dequantize_tiles + cuBLAS bf16 (gguf-plugin/gluon/interface.py:159-188,
@@ -61,8 +62,7 @@ __device__ __forceinline__ const uint8_t* col16(const uint8_t* plane, int r, int
 // ---- tile forms ------------------------------------------------------------------------------
 // A workgroup owns BM tokens x BN weight rows (BN / 64 tiles of one shard) and walks K in steps of
 // 64.  Forms: 256 x 256 with 8 waves (two per SIMD, one workgroup per CU: M > 128), 128 x 128 /
-// 64 x 128 with 4 waves (two workgroups per CU: M 65..128 / 33..64) and 32 x 128 with 4 waves side
-// by side (three workgroups per CU: M 17..32).  Each wave owns a block of
+// 64 x 128 with 4 waves (two workgroups per CU: M 65..128 / 33..64).  Each wave owns a block of
 // 32 x 32 v_mfma_f32_32x32x16_bf16 outputs.  Per step each thread decodes 32 weights of one row
 // (two runs of 16 at step-local offsets OFF0 / OFF1, per type) and, in the forms that stage x
 // through registers, stores activations of one token (the others load x straight into LDS); the
@@ -397,7 +397,7 @@ struct Geo {
   static constexpr int CH = MB * NB * 4;                          // 16-byte accumulator chunks per thread
   static constexpr int SLOT = BM * BN;                            // floats per partial slot
   static constexpr int LDS = 2 * (BM * XLD + BN * GB_LD) * 2;     // double-buffered x and weights
-  static constexpr int WPE = BM <= 32 ? 3 : 2;                    // waves per SIMD kept resident
+  static constexpr int WPE = 2;                                   // waves per SIMD kept resident
   static_assert(BN * 2 == NT, "one thread per (weight row, part)");
   static_assert(AV >= 1 && 8 % AV == 0, "x chunks per thread");
   static_assert(!XDMA || (XI >= 1 && XI * NW * 8 == BM), "whole 8-row x loads per wave");
@@ -407,12 +407,11 @@ struct Geo {
 typedef Geo<256, 256, 4, 2, 2, 2> GeoBig;          // M > 128: 8 waves, one workgroup per CU
 typedef Geo<128, 128, 2, 2, 1, 2, true> GeoMid;    // 65..128 tokens: 4 waves, two workgroups per CU
 typedef Geo<64, 128, 2, 2, 1, 2> GeoSmall;         // 33..64 tokens
-typedef Geo<32, 128, 1, 4, 1, 2> GeoTiny;          // 17..32 tokens: 4 waves side by side, three workgroups per CU
 // x by direct-to-LDS loads (XDMA), measured against the register path on both 34816 x 5120 and
 // 5120 x 17408 shards for all eleven types: the 128 x 128 form 1-13% faster at M = 100 (every
 // type but Q5_0, even there); the 256 x 256 form 3-7% faster for Q3_K, Q4_K and IQ4_NL at
-// M = 512 / 2048 and 1-6% slower for Q4_0, Q5_0, Q8_0, Q2_K and Q6_K; the 64 x 128 and 32 x 128
-// forms even to 2-7% slower.  The direct loads go one step ahead (the register path's big form
+// M = 512 / 2048 and 1-6% slower for Q4_0, Q5_0, Q8_0, Q2_K and Q6_K; the 64 x 128 form even to
+// 2-7% slower.  The direct loads go one step ahead (the register path's big form
 // two), and the compiler completes them with a vmcnt(0) at the step's barrier, which also waits
 // for the weight loads in flight; a variant that issued them from inline asm (no compiler wait)
 // with weights three steps ahead measured no faster.
@@ -831,6 +830,207 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(GE::WPE)
   }
 }
 
+// ---- the mid form: 17..32 batch rows -----------------------------------------------------------
+// The GEMV's work split (one workgroup per descriptor row: a 64-row tile and a k-range of
+// super-blocks that its waves divide; tiles shared by several rows combine fp32 partials in
+// split order, the last to arrive writing y) with the GEMM's arithmetic: each weight decoded
+// once to bf16 (round-to-nearest-even of the exact fp32 value, the same B2 decoders) straight
+// into registers, and v_mfma_f32_32x32x16_bf16 over all 32 tokens.  No LDS staging of weights or
+// x and no barrier in the main loop: lane l acts as decoder thread (row l % 32 and 32 + l % 32,
+// part l / 32) of each 64-weight step, which is exactly the MFMA's B-operand layout (column
+// l % 32, k-chunk l / 32); its A operand is x of token l % 32 at the same eight k, read from
+// global memory (L2) at the step that uses it.  One step of weights is in flight while the
+// previous one is decoded.  Measured against the 32 x 128 GEMM tile form it replaces (Q4_K
+// gate_up / qkv / o_proj / down at M = 32: 0.87 / 0.86 / 0.84 / 0.76 of its time; Q2_K, Q8_0,
+// Q6_K down 0.80 / 0.77 / 0.86, IQ4_XS gate_up 0.94; Q6_K and Q8_0 gate_up 1.04).  Tried: weights
+// two steps ahead (more registers, fewer waves: 0-8% slower) and 64 tokens per wave (226-260
+// VGPRs: 23-45% slower than the 64 x 128 GEMM form, which keeps 33..64 rows).
+template <int T>
+__device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ xr, int kw0,
+                                         int kw1, int c, int r, const GTabs& tb, v16f (&acc)[2]) {
+  constexpr int REC = gqk_layout<T>::REC;
+  if (kw0 >= kw1) return;
+  // k offsets (within a 64-weight step) of the lane's four 8-weight chunks, in MFMA order
+  const int koff[4] = {B2<T>::off0(c), B2<T>::off0(c) + 8, B2<T>::off1(c), B2<T>::off1(c) + 8};
+  const int s0 = 4 * kw0, last = 4 * kw1 - 1;
+  struct Step { B2<T> w[2]; };
+  Step p0, p1;
+  auto load = [&](Step& p, int s) __attribute__((always_inline)) {
+    const uint8_t* rc = tbase + (int64_t)(s >> 2) * (64 * REC);
+    p.w[0].load(rc, r, s & 3, c);
+    p.w[1].load(rc, 32 + r, s & 3, c);
+  };
+  auto compute = [&](const Step& p, int s) __attribute__((always_inline)) {
+    v8bf a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = *(const v8bf*)(xr + (int64_t)s * 64 + koff[q]);
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const GS st = p.w[b].prep(s & 3, c);
+      uint32_t o[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p.w[b].out(st, s & 3, c, o, tb, i);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            a[q], __builtin_bit_cast(v8bf, v4u{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]}), acc[b], 0, 0, 0);
+    }
+  };
+  // loads are unconditional (clamped to the wave's last step, re-read from L2 at the tail)
+  load(p0, s0);
+  load(p1, min(s0 + 1, last));
+  for (int s = s0;; s += 2) {
+    compute(p0, s);
+    load(p0, min(s + 2, last));
+    if (s + 1 > last) break;
+    compute(p1, s + 1);
+    load(p1, min(s + 3, last));
+    if (s + 2 > last) break;
+  }
+}
+
+#define MID_RED_BYTES (3 * 2 * 16 * 64 * 4)   // the waves' sums combined in LDS (nw <= 4)
+
+template <int ONLY>
+__global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
+                                                       const uint16_t* __restrict__ x, int64_t ldx, int M,
+                                                       uint16_t* __restrict__ y, int64_t ldy,
+                                                       const uint16_t* __restrict__ bias, float* __restrict__ part,
+                                                       int* __restrict__ ctr) {
+  constexpr int MP = 32;   // tokens of the plan (partial slots [slot][64 rows][MP])
+  __shared__ __attribute__((aligned(16))) uint8_t lds[MID_RED_BYTES + GB_TAB_BYTES];
+  const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
+  const int type = dsc[D_TYPE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int c = lane >> 5, r = lane & 31;
+  GTabs tb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tb.kv[i] = (uint32_t)(c_kvalues[4 * i] + 128) | ((uint32_t)(c_kvalues[4 * i + 1] + 128) << 8) |
+               ((uint32_t)(c_kvalues[4 * i + 2] + 128) << 16) | ((uint32_t)(c_kvalues[4 * i + 3] + 128) << 24);
+  tb.grid = (uint32_t*)(lds + MID_RED_BYTES);
+  tb.sign = (uint4*)(lds + MID_RED_BYTES + 512 * 4);
+  if ((ONLY == 0 || ONLY == GQK_IQ3_S) && type == GQK_IQ3_S) {   // uniform over the workgroup
+    uint32_t* grid = (uint32_t*)(lds + MID_RED_BYTES);
+    uint4* sign = (uint4*)(lds + MID_RED_BYTES + 512 * 4);
+    for (int t = threadIdx.x; t < 512; t += blockDim.x) grid[t] = c_iq3s_grid[t];
+    for (int t = threadIdx.x; t < 256; t += blockDim.x) {
+      uint32_t m[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m[q] = (((t >> (2 * q)) & 1) << 15) | (((t >> (2 * q + 1)) & 1) << 31);
+      sign[t] = make_uint4(m[0], m[1], m[2], m[3]);
+    }
+    __syncthreads();
+  }
+  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
+  const int64_t tile = dsc[D_TILE0];
+  const int nb = dsc[D_NB], kb0 = dsc[D_KB0], nk = dsc[D_KB1] - kb0;
+  const int kw0 = kb0 + (wave * nk) / nw, kw1 = kb0 + ((wave + 1) * nk) / nw;
+  const uint16_t* xr = x + (int64_t)min(r, M - 1) * ldx;   // tokens past M: clamped, never stored
+  v16f acc[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
+#define RUN(T)                                                                                                 \
+  if ((ONLY == 0 || ONLY == T) && type == T)                                                                   \
+    mid_wave<T>(packed + off + tile * nb * (int64_t)(64 * gqk_layout<T>::REC), xr, kw0, kw1, c, r, tb, acc);
+  RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
+  RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
+#undef RUN
+
+  // combine the waves (fixed order) in wave 0
+  float* red = (float*)lds;   // [wave - 1][b][v][lane]
+  if (wave > 0)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[(((wave - 1) * 2 + b) * 16 + v) * 64 + lane] = acc[b][v];
+  __syncthreads();
+  if (wave > 0) return;
+  for (int w = 1; w < nw; ++w)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[b][v] += red[(((w - 1) * 2 + b) * 16 + v) * 64 + lane];
+
+  // C block b: lane -> weight row 32 b + r, tokens 8 (v / 4) + 4 c + v % 4
+  const int nvalid = dsc[D_NVALID];
+  const int64_t col0 = dsc[D_COL0];
+  auto store_y = [&](int b, const v16f& a) {
+    const int row = 32 * b + r;
+    if (row >= nvalid) return;
+    // the layer bias (bf16 per output column) joins before the one rounding to bf16
+    const float bv = bias != nullptr ? __builtin_bit_cast(float, (uint32_t)bias[col0 + row] << 16) : 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int t = 8 * (v >> 2) + 4 * c + (v & 3);
+      if (t < M) y[(int64_t)t * ldy + col0 + row] = __builtin_bit_cast(uint16_t, (__bf16)(a[v] + bv));
+    }
+  };
+  const int nc = dsc[D_NC];   // workgroups sharing this tile
+  if (nc == 1) {
+    store_y(0, acc[0]);
+    store_y(1, acc[1]);
+    return;
+  }
+  // Split-K exchange, as in the GEMV: the nc partials of a tile in slots D_SLOT0 .. + nc - 1 as
+  // [slot][64 rows][32 tokens], moved by device-coherent (sc1) 16-byte buffer accesses only; the
+  // stores complete before the arrival count, and the last workgroup to arrive sums the slots in
+  // split order, writes y and resets the counter for the next launch.
+  const int sp = dsc[D_SPLIT], ctr_i = dsc[D_CTR];
+  float* tp = part + (int64_t)dsc[D_SLOT0] * 64 * MP;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, nc * 64 * MP * 4, GQK_GB_WORD3);
+  auto soff = [&](int q, int b, int g) { return ((q * 64 + 32 * b + r) * MP + 8 * g + 4 * c) * 4; };
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      __builtin_amdgcn_raw_buffer_store_b128(v4f{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]},
+                                             rs, soff(sp, b, g), 0, GQK_GB_SC1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial stores are complete
+  int arrived = 0;
+  if (lane == 0) arrived = __hip_atomic_fetch_add(&ctr[ctr_i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  arrived = __shfl(arrived, 0);
+  if (arrived != nc - 1) return;
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    v16f sum;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sum[v] = 0.f;
+    for (int q = 0; q < nc; ++q) {
+      v4f t[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) t[g] = __builtin_amdgcn_raw_buffer_load_b128(rs, soff(q, b, g), 0, GQK_GB_SC1);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[4 * g + e] += t[g][e];
+    }
+    store_y(b, sum);
+  }
+  if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+}
+
+int launch_gemv_mid(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
+                    int M, int nw, void* y, int64_t ldy, const void* bias, float* part, int* ctr, hipStream_t st) {
+  if (nw < 1 || nw > 4) return GQK_ERR_FORM;
+  const dim3 grid(n_desc), block(64 * nw);
+  const uint16_t* xx = (const uint16_t*)x;
+  uint16_t* yy = (uint16_t*)y;
+  const uint16_t* bb = (const uint16_t*)bias;
+  switch (types_mask) {
+#define C(T) case T: hipLaunchKernelGGL((gemv_mid_kernel<T>), grid, block, 0, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, ctr); return GQK_OK;
+    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
+    default:
+      hipLaunchKernelGGL((gemv_mid_kernel<0>), grid, block, 0, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, ctr);
+  }
+  return GQK_OK;
+}
+
 // CUs of the current device, cached per device
 static int gb_cus() {
   static int cache[64] = {0};
@@ -845,20 +1045,19 @@ static int gb_cus() {
 }
 
 // persistent workgroups of a form: every one resident (the 256 form takes a whole CU's LDS)
-static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : bm == 32 ? 3 : 2); }
+static int gb_workgroups(int bm) { return gb_cus() * (bm == 256 ? 1 : 2); }
 static int gb_slot_floats(int bm) {
-  return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : bm == 64 ? GeoSmall::SLOT : GeoTiny::SLOT;
+  return bm == 256 ? GeoBig::SLOT : bm == 128 ? GeoMid::SLOT : GeoSmall::SLOT;
 }
 
 // Stream-K workgroups for R remainder tiles of S = 4 nb steps: at most G, at least 16 steps per
-// workgroup and at most 6 workgroups per tile (12 in the 32 x 128 form, whose partial tiles are
-// small).  The last contributor of a tile sums every other one's partial slot in dependent
-// device-scope round trips, so contributors cost more than the steps they take over: measured on
-// the 5120-row shards at M = 17..200, all G workgroups (13 per tile) took 33-110 us, 16 steps /
-// <= 6 per tile 22-70 us; tile-rich shards keep all G.  Up to 12 per tile: `down` (K = 17408) at
-// M = 20-32 4-6% faster, at M = 48-100 (the larger forms) 1-20% slower.
+// workgroup and at most 6 workgroups per tile.  The last contributor of a tile sums every other
+// one's partial slot in dependent device-scope round trips, so contributors cost more than the
+// steps they take over: measured on the 5120-row shards at M = 17..200, all G workgroups (13 per
+// tile) took 33-110 us, 16 steps / <= 6 per tile 22-70 us; tile-rich shards keep all G.  (Up to
+// 12 per tile measured 1-20% slower at M = 48-100.)
 static int64_t gb_stream_k_workgroups(int G, int64_t R, int nb, int bm) {
-  return std::max<int64_t>(1, std::min<int64_t>({(int64_t)G, R * 4 * nb / 16, (bm == 32 ? 12 : 6) * R}));
+  return std::max<int64_t>(1, std::min<int64_t>({(int64_t)G, R * 4 * nb / 16, 6 * R}));
 }
 
 // Workspace: ctr_bytes of counters (the plan's counter region: at least G ints), then the partial tiles.
@@ -876,7 +1075,7 @@ int64_t gemm_workspace(int bm, int n_desc, int M, int nb, int64_t ctr_bytes) {
 // 2 G - 2 partial slots of the form's tile.
 int64_t gemm_workspace_max() {
   int64_t m = 0;
-  for (int bm : {32, 64, 128, 256}) {
+  for (int bm : {64, 128, 256}) {
     const int G = gb_workgroups(bm);
     if (G <= 0) return -1;
     m = std::max<int64_t>(m, (int64_t)(2 * G - 2) * gb_slot_floats(bm) * 4);
@@ -921,7 +1120,6 @@ int launch_gemm(const uint8_t* packed, const int32_t* desc, int n_desc, int type
     case 256: return launch_sk<GeoBig>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     case 128: return launch_sk<GeoMid>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     case 64: return launch_sk<GeoSmall>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
-    case 32: return launch_sk<GeoTiny>(types_mask, n_desc, M, nb, st, packed, desc, xx, ldx, yy, ldy, bb, ctr_bytes, ws, ws_bytes);
     default: return GQK_ERR_FORM;
   }
 }

@@ -900,6 +900,7 @@ int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int type
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
+  if (G == 8) return launch_gemv_mid(packed, desc, n_desc, types_mask, x, ldx, M, nw, y, ldy, bias, partials, counters, st);
   switch (G) {
 #define L(GG)                                                                                              \
     if (one) launch_g<GG, true>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); \

@@ -8,9 +8,9 @@ the MI355X path without touching its linear method.
 Every call runs the HIP library (there is no CPU path).  Differences from the Gluon module, all
 at the level of what a caller can observe:
 
-* every GGUF type here has one kernel family for every row count (GEMV up to 16 rows, MFMA GEMM
-  above), so ``GLUON_DEQUANT_TYPES`` is empty and the row-count limits only matter to callers
-  that choose paths by them;
+* every GGUF type here has one kernel family for every row count (GEMV up to 16 rows, the mid
+  form up to 32, MFMA GEMM above), so ``GLUON_DEQUANT_TYPES`` is empty and the row-count limits
+  only matter to callers that choose paths by them;
 * ``gluon_mul_mat`` on raw rows (``gguf-plugin/gluon/interface.py:74-80``) repacks a weight to the
   tile layout on its first call and keeps the tiles and launch plans in a cache attached to the
   weight's base tensor (the storage the view belongs to, e.g. the layer's parameter), keyed by the
@@ -47,7 +47,7 @@ GLUON_INT8_TYPES = frozenset()                   # no int8-activation form: acti
 GLUON_TILE_TYPES = frozenset(ops.GGUF_TYPES)     # the types the loader holds in the tile layout
 GLUON_DEQUANT_TYPES = frozenset()                # no run falls back to dequantize + a library GEMM
 GLUON_MAX_ROWS = 16                              # rows of the decode GEMV form
-GLUON_MAX_ROWS_GROUPED = 32                      # rows of the smallest GEMM tile form
+GLUON_MAX_ROWS_GROUPED = 32                      # rows of the streaming forms (GEMV, then the mid form)
 GLUON_ARRIVAL_ROWS = 128                         # rows of the 128 x 128 GEMM tile form
 
 

@@ -32,11 +32,12 @@ TYPE_NAMES = {Q4_0: "Q4_0", Q5_0: "Q5_0", Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_
 # unquantized GGML types the plugin multiplies as they are (F32, F16, BF16)
 UNQUANTIZED_TYPES = (0, 1, 30)
 
-# batch-row buckets of a grouped layer: GEMV plans serve M <= 4, 8, 16; GEMM above
-GEMV_BUCKETS = (4, 8, 16)
-# GEMM plans: 32 / 64 x 128 tiles (17..32 / 33..64 rows), 128 x 128 (65..128), 129..384, 385..512 and
-# 513..768 (256 x 256, or 128 x 128 for a layer with few 256-row groups), 256 x 256 above
-GEMM_PLAN_M = (32, 64, 128, 384, 512, 768, 769)
+# batch-row buckets of a grouped layer: the streaming plans serve M <= 4, 8, 16 (GEMV) and 17..32
+# (the mid form); GEMM above
+GEMV_BUCKETS = (4, 8, 16, 32)
+# GEMM plans: 64 x 128 tiles (33..64 rows), 128 x 128 (65..128), 129..384, 385..512 and 513..768
+# (256 x 256, or 128 x 128 for a layer with few 256-row groups), 256 x 256 above
+GEMM_PLAN_M = (64, 128, 384, 512, 768, 769)
 
 _DTYPES = {torch.float32: _lib.GQK_DTYPE_F32, torch.bfloat16: _lib.GQK_DTYPE_BF16, torch.float16: _lib.GQK_DTYPE_F16}
 

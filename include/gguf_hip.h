@@ -28,8 +28,9 @@ extern "C" {
 #define GQK_ERR_HIP (-4)   /* HIP runtime error at launch */
 #define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
 
-#define GQK_FORM_GEMV 1 /* M <= 16, every type: in-register decode GEMV (MFMA per scale group) */
-#define GQK_FORM_GEMM 2 /* M > 16: LDS-dequant bf16 MFMA GEMM (any M) */
+#define GQK_FORM_GEMV 1 /* M <= 32, every type: streaming forms over (tile, k-range) rows: the in-register
+                           decode GEMV up to 16 rows, the mid form (g = 8) for 17..32 */
+#define GQK_FORM_GEMM 2 /* M > 32: LDS-dequant bf16 MFMA GEMM (any M) */
 
 #define GQK_CTR_BYTES 262144 /* the arrival-counter region at the start of every workspace */
 
@@ -49,8 +50,8 @@ typedef struct gqk_shard {
 typedef struct gqk_plan_info {
   int32_t form;       /* GQK_FORM_GEMV or GQK_FORM_GEMM */
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
-  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4) */
-  int32_t bm;         /* GEMM: tokens per tile (32, 64, 128, 256); GEMV: 1 when every wave streams
+  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4; 8 = the mid form, 17..32 rows) */
+  int32_t bm;         /* GEMM: tokens per tile (64, 128, 256); GEMV (g <= 2): 1 when every wave streams
                          exactly one 256-weight record (the launch takes the pipeline-free kernel) */
   int32_t split;      /* GEMV: most workgroups sharing one tile (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
@@ -106,7 +107,7 @@ int gqk_unrepack(const void* tiles, int ggml_type, int64_t n, int64_t K, void* W
  * the device.  cus: compute units of the device the plan is for (256 on MI355X); 0 asks the HIP
  * runtime for the current device's count (initialising the runtime; 256 when no device is
  * visible).  target_wgs > 0 overrides the GEMV heuristic's target of resident waves (0 = eight per
- * CU), from which the waves per workgroup and the split-K factor follow.  GEMM plans (M > 16)
+ * CU), from which the waves per workgroup and the split-K factor follow.  GEMM plans (M > 32)
  * take their tile form from M and, at 129..384 rows (129..768 for K <= 8192), from the layer's
  * size against the CU count.  Replaces prepare_grouped_layer / descriptors / grouped_split_for
  * (gguf-plugin/gluon/tiles_grouped.py:237-299). */
@@ -145,9 +146,9 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
  * once per device on the first call, which also clears its counters with a fill kernel on
  * `stream`).  Allocates nothing.  A plan that needs more workspace at this M is refused with
  * GQK_ERR_SHAPE: GEMM plans above 64 rows on large layers, and GEMV plans whose split-K partials
- * exceed the 32 MiB (those are 64 rows x m_max tokens x 4 bytes per partial slot: at most 8,192
- * slots at m_max = 16, 32,768 at m_max = 4; e.g. a layer of 2,374 tiles at K = 16384 split 16 ways
- * at M <= 4 needs ~39 MB).  Every call on one GPU shares that
+ * exceed the 32 MiB (those are 64 rows x m_max tokens x 4 bytes per partial slot: at most 4,096
+ * slots at m_max = 32, 8,192 at 16, 32,768 at 4; e.g. a layer of 2,374 tiles at K = 16384 split 16
+ * ways at M <= 4 needs ~39 MB).  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (other streams, other threads) race. */
 #define GQK_NOALLOC_SCRATCH_BYTES (GQK_CTR_BYTES + 33554432)
 int gqk_linear_noalloc(const void* packed, const int32_t* desc_dev, const gqk_plan_info* info, const void* x,

@@ -281,7 +281,7 @@ def test_plan_random_layers_stay_in_bounds():
             groups = sum(((n + 63) // 64 + 3) // 4 for _, n, _ in shards)
             short = M <= 384 or (M <= 768 and K <= 32 * 256)
             big = 256 if not short or groups * ((M + 255) // 256) * 4 >= 256 else 128
-            assert info.form == 2 and info.bm == (32 if M <= 32 else 64 if M <= 64 else 128 if M <= 128 else big)
+            assert info.form == 2 and M > 32 and info.bm == (64 if M <= 64 else 128 if M <= 128 else big)
             per = 4 if info.bm == 256 else 2
             seen = {}
             for row in d:
@@ -325,13 +325,14 @@ def test_plan_descriptor_rows_mixed_layer():
     assert g[:, 4].tolist() == [2, 4, 1] and g[:, 9].tolist() == [70, 256, 44]
     assert g[:, 8].tolist() == [0, 70, 326]
     assert _plan([(21, 70, 0), (12, 300, off2)], K, 40)[0].bm == 64
-    assert _plan([(21, 70, 0), (12, 300, off2)], K, 20)[0].bm == 32
+    info = _plan([(21, 70, 0), (12, 300, off2)], K, 20)[0]             # 17..32 rows: the mid form
+    assert (info.form, info.g, info.m_max, info.bm) == (1, 8, 32, 0)
 
 
 def test_plan_buckets():
     from gguf_hip import ops
 
-    for M, g in ((1, 1), (4, 1), (5, 2), (8, 2), (9, 4), (16, 4)):
+    for M, g in ((1, 1), (4, 1), (5, 2), (8, 2), (9, 4), (16, 4), (17, 8), (32, 8)):
         info, _ = _plan([(12, 512, 0)], 512, M)
         assert info.form == 1 and info.g == g and info.m_max == 4 * g
     assert ops._pick_plan([], 1) == 0 and ops._pick_plan([], 16) == 2
@@ -341,13 +342,15 @@ def test_plan_buckets():
     assert ops._pick_plan([], 385) == 7 and ops._pick_plan([], 512) == 7
     assert ops._pick_plan([], 513) == 8 and ops._pick_plan([], 768) == 8
     assert ops._pick_plan([], 769) == 9 and ops._pick_plan([], 8192) == 9
-    # every type, the table types (IQ4_NL / IQ4_XS / IQ3_S) included, stays on the GEMV up to 16 rows
+    # every type, the table types (IQ4_NL / IQ4_XS / IQ3_S) included, stays on the GEMV up to 16 rows,
+    # then on the mid form up to 32
     for wt in (20, 23, 21):
-        i9, i16, i17 = (_plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17))
-        assert (i9.form, i9.g, i16.form, i16.g, i17.form, i17.bm) == (1, 4, 1, 4, 2, 32)
+        i9, i16, i17, i33 = (_plan([(wt, 512, 0)], 512, m)[0] for m in (9, 16, 17, 33))
+        assert (i9.form, i9.g, i16.form, i16.g, i17.form, i17.g, i33.form, i33.bm) == (1, 4, 1, 4, 1, 8, 2, 64)
     off = ops.tiles_bytes(12, 512, 512)
     assert _plan([(12, 512, 0), (23, 64, off)], 512, 12)[0].form == 1
-    for M, bm in ((17, 32), (32, 32), (33, 64), (64, 64), (65, 128), (128, 128), (129, 128), (384, 128),
+    assert _plan([(12, 512, 0), (23, 64, off)], 512, 30)[0].form == 1
+    for M, bm in ((33, 64), (64, 64), (65, 128), (128, 128), (129, 128), (384, 128),
                   (512, 128), (768, 128), (769, 256), (2048, 256)):
         assert _plan([(12, 512, 0)], 512, M)[0].bm == bm
     # 129..384 rows: 256 x 256 tiles once the 256-row groups times the token blocks reach a quarter

@@ -116,7 +116,8 @@ def test_gemv_tail_tiles_split(dev, wt):
 def test_graph_replay_matches_eager(dev):
     """The grouped op captured in one HIP graph, as a serving loop (and bench.py) runs it: the
     GEMV with split-K partials and in-kernel counters, the GEMV with a split tail, with a fused
-    bias, and the stream-K GEMM in its 32-row and 256-row forms.  Five replays, each after new x
+    bias, the mid form (17..32 rows) with split K, and the stream-K GEMM in its 64-row and 256-row
+    forms.  Five replays, each after new x
     is copied into the captured inputs, followed by eager launches of the same layers (sharing
     the layers' workspaces) and a host synchronisation: every replay is bit-identical to the
     eager result on the same x, which matches the oracle, and the counters end at zero (they are
@@ -128,7 +129,8 @@ def test_graph_replay_matches_eager(dev):
         (G.Q4_K, 900, 12 * 256, 8, 0, False),        # GEMV, split K
         (G.Q6_K, 900, 12 * 256, 1, 0, True),         # GEMV, split K, fused bf16 bias
         (G.IQ4_XS, 64 * 9 + 17, 16 * 256, 5, 16, False),   # GEMV, whole tiles + split tail
-        (G.Q5_K, 1000, 2048, 20, 0, False),          # GEMM 32 x 128, stream-K only
+        (G.Q5_K, 1000, 2048, 20, 0, False),          # mid form, split K
+        (G.Q6_K, 1000, 2048, 40, 0, False),          # GEMM 64 x 128, stream-K only
         (G.Q4_K, 1000, 2048, 300, 0, True),          # GEMM 256 x 256, stream-K, bias
     ]
     layers, xs, biases, wfs = [], [], [], []
@@ -141,7 +143,7 @@ def test_graph_replay_matches_eager(dev):
     for gl, (wt, n, K, M, tw, _) in zip(layers, cases):
         info = gguf_hip.ops.GqkPlanInfo.from_tuple(
             gl.plans[gguf_hip.ops._pick_plan(gl.plans, M) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
-        assert info.form == (1 if M <= 8 else 2) and (M > 8 or info.split > 1), (G.NAMES[wt], M)
+        assert info.form == (1 if M <= 32 else 2) and (M > 32 or info.split > 1), (G.NAMES[wt], M)
 
     def run():
         return [gguf_hip.mul_mat_grouped(x, gl, b) for x, gl, b in zip(xs, layers, biases)]
@@ -200,7 +202,7 @@ def test_random_layers_match_reference(dev):
 
 
 def test_one_workspace_serves_every_form(dev):
-    """One layer workspace across the GEMV (split tiles) and the three GEMM forms (stream-K
+    """One layer workspace across the GEMV and mid form (split tiles) and the GEMM forms (stream-K
     partials) in an order where each form's partials would land on another form's counters if
     the counter regions differed: every call matches the oracle and repeats bit-identically,
     and the counters end at zero."""
@@ -212,7 +214,7 @@ def test_one_workspace_serves_every_form(dev):
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K], target_wgs=2048)
     wf = G.dequantize(raw, G.Q4_K)
     first = {}
-    for M in (300, 1, 40, 100, 300, 8, 40, 1, 100):
+    for M in (300, 1, 40, 24, 100, 300, 8, 24, 40, 1, 100):
         x = _x(M, K, 9000 + M, dev)
         y = gguf_hip.mul_mat_grouped(x, gl)
         if M not in first:
@@ -241,14 +243,14 @@ def test_mixed_layer_one_launch(dev):
     wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
     gl = gguf_hip.pack_layer(Ws, [n for _, n in shards], [wt for wt, _ in shards], target_wgs=1)
     singles = [gguf_hip.pack_layer([W], [n], [wt], target_wgs=1) for W, (wt, n) in zip(Ws, shards)]
-    for M in (1, 6, 12, 20, 40, 200):   # 12: IQ3_S / Q8_0 / IQ4_XS in the 16 x 16 x 32 form beside the others
+    for M in (1, 6, 12, 20, 40, 200):   # 12: IQ3_S / Q8_0 / IQ4_XS in the 16 x 16 x 32 form; 20: the mid form
         x = _x(M, K, 3000 + M, dev)
         y = gguf_hip.mul_mat_grouped(x, gl)
         assert G.rel_err(y.float().cpu().numpy(), _ref(x, wf)) < TOL, M
         col = 0
         for s, (wt, n) in zip(singles, shards):
             ys = gguf_hip.mul_mat_grouped(x, s)
-            if M <= 16:
+            if M <= 32:                     # the streaming forms (GEMV, mid): the same split per tile
                 assert torch.equal(y[:, col:col + n], ys), (M, G.NAMES[wt])
             else:
                 a, b = y[:, col:col + n].float(), ys.float()
@@ -395,7 +397,7 @@ def test_fused_bias(dev):
     gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [G.Q4_K])
     zero = torch.zeros(n, dtype=torch.bfloat16, device=dev)
     bias = (torch.randn(n, device=dev) * 4).to(torch.bfloat16)
-    for M in (1, 8, 16, 40, 100, 300):
+    for M in (1, 8, 16, 24, 40, 100, 300):
         x = _x(M, K, 6000 + M, dev)
         y0 = gguf_hip.mul_mat_grouped(x, gl)
         assert torch.equal(gguf_hip.mul_mat_grouped(x, gl, zero), y0), M
@@ -444,13 +446,13 @@ def test_baseline_config1_q8_0(dev):
 
 @pytest.mark.parametrize("n,K,M", [(1000, 2048, 300), (1000, 2048, 2148), (16384, 512, 1100),
                                    (1000, 2048, 40), (16384, 512, 100), (70000, 256, 64), (70000, 256, 120),
-                                   (1000, 2048, 20), (5120, 5120, 32), (200000, 256, 30)],
+                                   (1000, 2048, 33), (5120, 5120, 48), (200000, 256, 40)],
                          ids=str)
 @pytest.mark.parametrize("wt", [G.Q5_K, G.Q4_K, G.Q8_0], ids=lambda t: G.NAMES[t])
 def test_gemm_stream_k_schedule(dev, n, K, M, wt):
     """The GEMM forms' persistent schedule (256 x 256 tiles above 128 rows, except 129..384 rows of a
-    layer with few 256-row groups, which keep 128 x 128 (1000 rows at M = 300 here); 128 x 128,
-    64 x 128 and 32 x 128 at 65..128, 33..64 and 17..32): whole tiles dealt to the workgroups, the remainder
+    layer with few 256-row groups, which keep 128 x 128 (1000 rows at M = 300 here); 128 x 128 and
+    64 x 128 at 65..128 and 33..64): whole tiles dealt to the workgroups, the remainder
     tiles' k-steps split over up to all of them (stream-K, >= 16 steps each, <= 6 per tile) and
     combined in k order by the last contributor.  Small grids are all remainder; the 16384-row
     case at M=1100 and the 70000- and 200000-row cases mix both phases.  The 256 x 256 tile runs
@@ -480,7 +482,8 @@ def test_gemm_stream_k_schedule(dev, n, K, M, wt):
 def test_strided_activations_every_form(dev, wt):
     """x as a column slice of a wider buffer (row stride K + 24, 16-byte aligned start) goes to the
     kernels as is, in every form: GEMV (M <= 16; at 9-16 rows Q8_0 / IQ4_XS read it straight from
-    global memory in the 16 x 16 x 32 form) and the four GEMM tiles, with x staged through
+    global memory in the 16 x 16 x 32 form), the mid form (17..32 rows, x read straight from global
+    memory) and the three GEMM tiles, with x staged through
     registers (Q6_K, Q8_0 in the 256 x 256 form) or by direct-to-LDS loads (the 128 x 128 form,
     Q4_K in the 256 x 256 form), full and partial token blocks.  Each result is bit-identical to
     the one from a contiguous copy of x."""
@@ -500,3 +503,38 @@ def test_strided_activations_every_form(dev, wt):
         ref = xs.float() @ wf.T
         e = float(((y.float() - ref).abs() / ref.abs().amax(dim=1, keepdim=True).clamp(min=1e-30)).amax())
         assert e < TOL, (G.NAMES[wt], M, e)
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_mid_form_17_to_32_rows(dev, wt):
+    """The mid form (17..32 rows: the GEMV's descriptor rows and split-K exchange, weights decoded
+    to bf16 in registers, MFMA 32x32x16): every type on a ragged shard at several split factors
+    (the wave target) against the oracle (tolerance 1e-2 of each row's max |y|), bit-identical
+    repeats, a fused bias, a column slice of a wider output, and the counters back at zero."""
+    import gguf_hip
+
+    rng = np.random.default_rng(800 + wt)
+    n, K = 197, 24 * 256
+    raw = G.random_blocks(rng, n, K, wt)
+    wf = G.dequantize(raw, wt)
+    W = torch.from_numpy(raw).to(dev)
+    bias = (torch.randn(n, device=dev) * 2).to(torch.bfloat16)
+    for target in (0, 1, 13, 64):
+        gl = gguf_hip.pack_layer([W], [n], [wt], target_wgs=target)
+        for M in (17, 23, 32):
+            i = gguf_hip.ops._pick_plan(gl.plans, M)
+            info = gguf_hip.ops.GqkPlanInfo.from_tuple(gl.plans[i * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
+            assert info.form == 1 and info.g == 8 and info.m_max == 32, (target, M)
+            x = _x(M, K, 8100 + M, dev)
+            y = gguf_hip.mul_mat_grouped(x, gl)
+            e = G.rel_err(y.float().cpu().numpy(), _ref(x, wf))
+            assert e < TOL, (G.NAMES[wt], target, M, e)
+            assert torch.equal(gguf_hip.mul_mat_grouped(x, gl), y), (target, M)
+            yb = gguf_hip.mul_mat_grouped(x, gl, bias).float().cpu().numpy()
+            assert G.rel_err(yb, _ref(x, wf) + bias.float().cpu().numpy()[None]) < TOL, (target, M)
+            wide = torch.full((M, n + 40), 7.0, dtype=torch.bfloat16, device=dev)
+            gguf_hip.mul_mat_grouped(x, gl, out=wide[:, 24:24 + n])
+            assert torch.equal(wide[:, 24:24 + n], y) and bool((wide[:, :24] == 7).all())
+            assert bool((wide[:, 24 + n:] == 7).all()), (target, M)
+        torch.cuda.synchronize()
+        assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
