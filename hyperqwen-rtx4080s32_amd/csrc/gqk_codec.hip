@@ -287,7 +287,68 @@ __device__ __forceinline__ void every_plane_word(int tid, F&& f) {
   }
 }
 
-// The 64 raw records of a chunk from its plane-major words (16-byte loads), into raw[row][REC] in LDS.
+// ---- Q6_K: the six-bit values re-packed per scale group (gqk_q6_pos) <-> GGUF's ql / qh ----------
+// q of weight k of a raw record (ql[128] | qh[64], kq_ref.py:69-79): 4 low bits from ql, 2 from qh
+__device__ __forceinline__ uint32_t q6_raw(const uint8_t* rec, int k) {
+  const int hh = k >> 7, l = k & 127;
+  const uint32_t lo = (rec[64 * hh + (l & 63)] >> (4 * (l >> 6))) & 0xF;
+  const uint32_t hi = (rec[128 + 32 * hh + (l & 31)] >> (2 * (l >> 5))) & 3;
+  return lo | (hi << 4);
+}
+// q of weight k of a re-packed record
+__device__ __forceinline__ uint32_t q6_packed(const uint8_t* rec, int k) {
+  const int g = k >> 4, j = k & 15;
+  if (j < 12) return rec[gqk_q6_pos(g, j >> 2, j & 3)] & 63;
+  uint32_t v = 0;
+#pragma unroll
+  for (int m = 0; m < 3; ++m) v |= (uint32_t)(rec[gqk_q6_pos(g, m, j - 12)] >> 6) << (2 * m);
+  return v;
+}
+// In place on the chunk's 64 records in LDS (raw[row][REC]): TO_PACKED re-packs bytes 0..191 of
+// every record, else restores GGUF's ql / qh.  Every thread computes its share into registers
+// before any is written (barriers between), so the pass reads only the old layout.
+template <bool TO_PACKED>
+__device__ __forceinline__ void q6_convert(uint8_t* raw, int tid) {
+  constexpr int REC = 210, PER = 64 * 48 / 256;   // 48 dwords of 192 bytes per row, 12 per thread
+  uint32_t v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int it = tid + 256 * k, r = it / 48, w = it % 48;
+    const uint8_t* rec = raw + r * REC;
+    uint32_t d = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = 4 * w + i;   // output byte
+      uint32_t byte;
+      if (TO_PACKED) {             // byte b = gqk_q6_pos(g, m, i'): low 6 bits of q[16 g + 4 m + i'], top 2 of q[16 g + 12 + i']
+        const int col = b >> 4, a = col / 3, m = col % 3, g = 4 * a + ((b >> 2) & 3), ii = b & 3;
+        byte = (q6_raw(rec, 16 * g + 4 * m + ii) & 63) | (((q6_raw(rec, 16 * g + 12 + ii) >> (2 * m)) & 3) << 6);
+      } else if (b < 128) {        // ql byte b: low nibbles of weights 128 hh + p and 128 hh + 64 + p
+        const int hh = b >> 6, p = b & 63;
+        byte = (q6_packed(rec, 128 * hh + p) & 15) | ((q6_packed(rec, 128 * hh + 64 + p) & 15) << 4);
+      } else {                     // qh byte: the high pairs of weights 128 hh + p + 32 t
+        const int hh = (b - 128) >> 5, p = (b - 128) & 31;
+        byte = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) byte |= (q6_packed(rec, 128 * hh + p + 32 * t) >> 4) << (2 * t);
+      }
+      d |= byte << (8 * i);
+    }
+    v[k] = d;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int it = tid + 256 * k, r = it / 48, w = it % 48;
+    uint8_t* rec = raw + r * REC;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rec[4 * w + i] = (uint8_t)(v[k] >> (8 * i));
+  }
+  __syncthreads();
+}
+
+// The 64 raw records of a chunk from its plane-major words (16-byte loads), into raw[row][REC] in
+// LDS (Q6_K's six-bit values converted back to ql / qh before the function returns).
 template <int T>
 __device__ __forceinline__ void chunk_to_raw(const uint4* __restrict__ in, uint8_t* raw, int tid) {
   constexpr int REC = gqk_planes<T>::v.rec;
@@ -302,6 +363,10 @@ __device__ __forceinline__ void chunk_to_raw(const uint4* __restrict__ in, uint8
     }
   };
   every_plane_word<T>(tid, scatter);
+  if constexpr (T == GQK_Q6_K) {
+    __syncthreads();
+    q6_convert<false>(raw, tid);
+  }
 }
 
 template <int T, bool TO_TILES, bool WIDE>
@@ -328,6 +393,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t* __restrict__
       }
     }
     __syncthreads();
+    if constexpr (T == GQK_Q6_K) q6_convert<true>(raw, tid);
     uint4* out = (uint4*)(dst + chunk * CB);
     auto gather = [&](int wi, auto&& at) {
       uint32_t v[4] = {0, 0, 0, 0};

@@ -62,10 +62,19 @@ struct gqk_type {
   X(GQK_Q3_K,  256, 110, 110, 4, {{64, 1, 32, 64, 0}, {32, 1, 0, 32, 0}, {12, 1, 96, 12, 0}, {2, 1, 108, 2, 0}}) \
   X(GQK_Q4_K,  256, 144, 144, 2, {{128, 1, 16, 128, 0}, {16, 1, 0, 16, 0}})                          \
   X(GQK_Q5_K,  256, 176, 176, 3, {{128, 1, 48, 128, 0}, {32, 1, 16, 32, 0}, {16, 1, 0, 16, 0}})        \
-  X(GQK_Q6_K,  256, 210, 210, 4, {{128, 1, 0, 128, 0}, {64, 1, 128, 64, 0}, {16, 1, 192, 16, 0}, {2, 1, 208, 2, 0}}) \
+  X(GQK_Q6_K,  256, 210, 210, 3, {{192, 1, 0, 192, 0}, {16, 1, 192, 16, 0}, {2, 1, 208, 2, 0}})       \
   X(GQK_IQ4_NL, 32, 18,  144, 2, {{128, 8, 2, 16, 18}, {16, 8, 0, 2, 18}})                            \
   X(GQK_IQ3_S, 256, 110, 110, 5, {{64, 1, 2, 64, 0}, {32, 1, 74, 32, 0}, {8, 1, 66, 8, 0}, {4, 1, 106, 4, 0}, {2, 1, 0, 2, 0}}) \
   X(GQK_IQ4_XS, 256, 136, 136, 2, {{128, 1, 8, 128, 0}, {8, 1, 0, 8, 0}})
+
+// Q6_K's first plane is not a byte gather: its 192 bytes per row (GGUF's ql[128] and qh[64]) hold
+// the 256 six-bit values q = lo | hi << 4 re-packed per 16-weight scale group g, as three dwords
+// P0..P2 whose bytes i carry q[16 g + 4 m + i] & 63 (dword m) in bits 0..5 and bits 2m, 2m + 1 of
+// q[16 g + 12 + i] in bits 6..7.  A decoder takes four 6-bit values with one AND (P_m & 0x3F3F3F3F)
+// and the last four from the three top-bit pairs.  The dwords of groups 4a .. 4a + 3 fill the
+// plane's columns 3a .. 3a + 2: column 3a + m holds P_m of group 4a + d as its dword d.  The repack
+// builds this from the raw record in LDS, and the unrepack / tile dequantizer invert it.
+__host__ __device__ constexpr int gqk_q6_pos(int g, int m, int i) { return 16 * (3 * (g >> 2) + m) + 4 * (g & 3) + i; }
 
 // The same table as compile-time constants per type (device code)
 struct gqk_type_c {
@@ -106,7 +115,7 @@ GQK_LAYOUT(GQK_Q2_K, 84, 0, 64, 80)
 GQK_LAYOUT(GQK_Q3_K, 110, 0, 64, 96, 108)
 GQK_LAYOUT(GQK_Q4_K, 144, 0, 128)
 GQK_LAYOUT(GQK_Q5_K, 176, 0, 128, 160)
-GQK_LAYOUT(GQK_Q6_K, 210, 0, 128, 192, 208)
+GQK_LAYOUT(GQK_Q6_K, 210, 0, 192, 208)
 GQK_LAYOUT(GQK_IQ4_NL, 144, 0, 128)
 GQK_LAYOUT(GQK_IQ3_S, 110, 0, 64, 96, 104, 108)
 GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)

@@ -104,11 +104,31 @@ def test_dequantize_32_block_types_any_k(dev, wt):
     assert np.array_equal(got, G.dequantize(raw, wt))
 
 
+def _q6_pack(rec):
+    """Q6_K's first tile plane: the 256 six-bit values q = lo | hi << 4 of GGUF's ql[128] / qh[64]
+    (kq_ref.py:69-79) re-packed per 16-weight group g as three dwords P_m, byte i of P_m = low six
+    bits of q[16 g + 4 m + i] | bits 2m, 2m + 1 of q[16 g + 12 + i] << 6, at byte
+    16 (3 (g // 4) + m) + 4 (g % 4) + i of the 192."""
+    ql, qh = rec[..., :128].astype(np.uint32), rec[..., 128:192].astype(np.uint32)
+    k = np.arange(256)
+    q = ((ql[..., 64 * (k >> 7) + (k & 63)] >> (4 * ((k & 127) >> 6))) & 0xF) | \
+        (((qh[..., 32 * (k >> 7) + (k & 31)] >> (2 * ((k & 127) >> 5))) & 3) << 4)
+    out = np.zeros(rec.shape[:-1] + (192,), np.uint8)
+    for g in range(16):
+        for m in range(3):
+            for i in range(4):
+                v = (q[..., 16 * g + 4 * m + i] & 63) | (((q[..., 16 * g + 12 + i] >> (2 * m)) & 3) << 6)
+                out[..., 16 * (3 * (g // 4) + m) + 4 * (g % 4) + i] = v
+    return out
+
+
 def _np_repack(raw, wt, n, K, planes, rec):
     nb = K // 256
     ntiles = -(-n // 64)
     rows = np.zeros((ntiles * 64, nb, rec), np.uint8)
     rows[:n] = raw.reshape(n, nb, rec)
+    if wt == G.Q6_K:
+        rows[:, :, :192] = _q6_pack(rows)
     out = np.zeros((ntiles, nb, 64 * rec), np.uint8)
     poff = 0
     for size, nseg, off, seglen, stride, width in planes:
