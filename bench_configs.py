@@ -47,10 +47,10 @@ def _copies(nbytes: int, floor_bytes: float, cap: int = 24) -> int:
     return max(2, min(cap, math.ceil(floor_bytes / nbytes)))
 
 
-def config3(torch, gguf_hip, random_shard, dev, ms: list[int]) -> None:
+def config3(torch, gguf_hip, random_shard, dev, ms: list[int], types=ALL_TYPES, shapes=CONFIG3_SHAPES) -> None:
     """every type alone as the (34816, 5120) and (5120, 17408) shards."""
-    for wt in ALL_TYPES:
-        for name, N, K in CONFIG3_SHAPES:
+    for wt in types:
+        for name, N, K in shapes:
             nbytes = random_shard(64, K, wt, dev).numel() // 64 * N
             gls = []
             for c in range(_copies(nbytes, 1.1e9)):
@@ -195,6 +195,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, required=True, choices=(3, 4, 5))
     ap.add_argument("--m", default="", help="comma-separated batch rows (default: the config's own list)")
     ap.add_argument("--layers", type=int, default=64, help="config 5: decoder layers")
+    ap.add_argument("--types", default="", help="config 3: comma-separated type names (default: all eleven)")
+    ap.add_argument("--shards", default="", help="config 3: comma-separated shard names, gate_up / down (default: both)")
     args = ap.parse_args()
 
     import torch
@@ -207,7 +209,10 @@ def main() -> int:
     default_ms = {3: "1,4,8,16,32", 4: "512,2048,8192", 5: "1,8,32,64"}[args.config]
     ms = [int(v) for v in (args.m or default_ms).split(",")]
     if args.config == 3:
-        config3(torch, gguf_hip, random_shard, dev, ms)
+        names = {v: k for k, v in gguf_hip.TYPE_NAMES.items()}
+        types = [names[t] for t in args.types.split(",")] if args.types else ALL_TYPES
+        shapes = [s for s in CONFIG3_SHAPES if not args.shards or s[0] in args.shards.split(",")]
+        config3(torch, gguf_hip, random_shard, dev, ms, types, shapes)
     elif args.config == 4:
         config4(torch, gguf_hip, random_shard, dev, ms)
     else:

@@ -92,12 +92,15 @@ __device__ __forceinline__ void split_bytes(uint32_t u, const Masks& k, uint32_t
 
 // Row r's slice of a plane of N bytes per row (N a multiple of 16).  Planes are column-major in
 // 16-byte columns: column i of row r sits at (i * 64 + r) * 16, so load i of a wave is one
-// contiguous 1 KiB access.
+// contiguous 1 KiB access.  The lane's offset enters as an unsigned 32-bit add to the column's
+// base, which lets the columns past the 4 KiB immediate range share the lane's offset register
+// (a signed (i * 64 + r) * 16 gave each such column a 64-bit address of its own, and Q6_K's
+// twelve columns spilled at three waves per SIMD).
 template <int N>
 __device__ __forceinline__ void ldp(uint32_t* dst, const uint8_t* plane, int r) {
 #pragma unroll
   for (int i = 0; i < N / 16; ++i) {
-    uint4 v = *(const uint4*)(plane + (i * 64 + r) * 16);
+    uint4 v = *(const uint4*)(plane + i * 1024 + (uint32_t)(r * 16));
     dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
   }
 }
@@ -560,25 +563,30 @@ __device__ __forceinline__ void gemv_pipeline(const uint8_t* __restrict__ tbase,
                                               const P& process) {
   typedef Dec<T> D;
   constexpr int MPAD = 4 * G, NI = (8 * MPAD + 63) / 64;
-  const int last = kw1 - 1;
-  auto rec = [&](int kb) { return tbase + (int64_t)min(kb, last) * (64 * D::REC); };
+  // the wave's record count in a scalar register: the loop's bound and the clamp of its follow-up
+  // loads take no VGPR (a VGPR bound spilled here, and its reload's vmcnt(0) at every back edge
+  // drained the loads in flight)
+  const int n = __builtin_amdgcn_readfirstlane(kw1 - kw0);
+  const uint8_t* tw = tbase + (int64_t)kw0 * (64 * D::REC);
+  const uint16_t* xw = x + (int64_t)kw0 * 256;
+  auto rec = [&](int i) { return tw + (int64_t)min(i, n - 1) * (64 * D::REC); };
   uint4 x0[NI][4], x1[NI][4];
   D r0, r1;
-  stage_load<MPAD>(x, ldx, M, kw0, lane, x0);
-  r0.load(rec(kw0), lane);
-  stage_load<MPAD>(x, ldx, M, min(kw0 + 1, last), lane, x1);
-  r1.load(rec(kw0 + 1), lane);
-  auto step = [&](D& r, uint4 (&xv)[NI][4], int kb) {
+  stage_load<MPAD>(xw, ldx, M, 0, lane, x0);
+  r0.load(rec(0), lane);
+  stage_load<MPAD>(xw, ldx, M, min(1, n - 1), lane, x1);
+  r1.load(rec(1), lane);
+  auto step = [&](D& r, uint4 (&xv)[NI][4], int i) {
     stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(wl, lane, xv);
     process(r);
-    stage_load<MPAD>(x, ldx, M, min(kb + 2, last), lane, xv);
-    r.load(rec(kb + 2), lane);
+    stage_load<MPAD>(xw, ldx, M, min(i + 2, n - 1), lane, xv);
+    r.load(rec(i + 2), lane);
   };
-  for (int kb = kw0;; kb += 2) {
-    step(r0, x0, kb);
-    if (kb + 1 > last) break;
-    step(r1, x1, kb + 1);
-    if (kb + 2 > last) break;
+  for (int i = 0;; i += 2) {
+    step(r0, x0, i);
+    if (i + 1 >= n) break;
+    step(r1, x1, i + 1);
+    if (i + 2 >= n) break;
   }
 }
 
