@@ -271,7 +271,7 @@ def main() -> int:
             info = plan_of(gls[0], Me)
             gbs = nb / (us * 1e-6) / 1e9
             extra.append({"M": Me, "type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
-                          "form": "gemv" if info.form == 1 else f"gemm{info.bm}", "GBps": round(gbs, 1),
+                          "form": (f"gemv_g{info.g}" if info.g <= 4 else "mid") if info.form == 1 else f"gemm{info.bm}", "GBps": round(gbs, 1),
                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
         del xe
     dom = max(rows, key=lambda r: r["us"])
