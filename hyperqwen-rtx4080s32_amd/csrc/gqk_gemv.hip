@@ -383,14 +383,15 @@ __device__ __forceinline__ v4f mfma1_bcast(int ab, float a, float b, v4f c) {
   return c;
 }
 
-// Which x operands a kernel broadcasts from registers (the MFMA operands, the group sums).  Q6_K
-// at G = 2 sits at the three-waves register bound: its streaming kernel broadcasts the operands
-// but reads the sums from LDS (with both it spills; as chosen, down / gate_up 4% / 1-2% faster
-// than neither), and its one-record kernel keeps both in LDS (0.2 us faster on qkv than either).
+// Which x operands a kernel broadcasts from registers (the MFMA operands, the group sums).  Every
+// kernel broadcasts both but Q6_K's one-record kernel at G = 2, which keeps both in LDS (0.2 us
+// faster on qkv than either; broadcasting both there measured -0.6..+1.5% on qkv / o_proj).  Q6_K's
+// streaming kernel at G = 2 takes both in 136 VGPRs (three waves per SIMD, no scratch): gate_up at
+// M = 6 / 8 2.4% and down 0.7% faster than with the sums from LDS.
 template <int G, int T, bool ONE>
 constexpr bool x_broadcast() { return !(G == 2 && T == GQK_Q6_K && ONE); }
 template <int G, int T, bool ONE>
-constexpr bool xq_broadcast() { return !(G == 2 && T == GQK_Q6_K); }
+constexpr bool xq_broadcast() { return x_broadcast<G, T, ONE>(); }
 
 template <int MPAD>
 struct WaveX {            // per-wave LDS: 64 slots x MPAD tokens x 8 B, then 16 + 8 group sums x MPAD
