@@ -761,9 +761,10 @@ __device__ __forceinline__ void gemv_wave_w16(const uint8_t* __restrict__ tbase,
     }
 }
 
-// Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 fits
-// three waves without spilling and runs faster there than at the allocator's own choice of two.
-// Q6_K at G = 4 measured 0-8% faster on gate_up and 2-4% slower on down at three.
+// Minimum waves per SIMD the register allocator must keep (1: no bound).  Q6_K at G = 2 runs
+// faster at three waves than at two; it now needs 136 VGPRs, so the bound only keeps a later
+// change from trading the third wave for registers.  (Q6_K at G = 4 takes 168 VGPRs, three waves,
+// on its own.)
 template <int G, int ONLY>
 constexpr int gemv_waves() {
   return (G == 2 && ONLY == GQK_Q6_K) ? 3 : 1;
