@@ -839,35 +839,57 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(GE::WPE)
 // super-blocks that its waves divide; tiles shared by several rows combine fp32 partials in
 // split order, the last to arrive writing y) with the GEMM's arithmetic: each weight decoded
 // once to bf16 (round-to-nearest-even of the exact fp32 value, the same B2 decoders) straight
-// into registers, and v_mfma_f32_32x32x16_bf16 over all 32 tokens.  No LDS staging of weights or
-// x and no barrier in the main loop: lane l acts as decoder thread (row l % 32 and 32 + l % 32,
-// part l / 32) of each 64-weight step, which is exactly the MFMA's B-operand layout (column
-// l % 32, k-chunk l / 32); its A operand is x of token l % 32 at the same eight k, read from
-// global memory (L2) at the step that uses it.  One step of weights is in flight while the
-// previous one is decoded.  Measured against the 32 x 128 GEMM tile form it replaces (Q4_K
-// gate_up / qkv / o_proj / down at M = 32: 0.87 / 0.86 / 0.84 / 0.76 of its time; Q2_K, Q8_0,
-// Q6_K down 0.80 / 0.77 / 0.86, IQ4_XS gate_up 0.94; Q6_K and Q8_0 gate_up 1.04).  Tried: weights
-// two steps ahead (more registers, fewer waves: 0-8% slower) and 64 tokens per wave (226-260
-// VGPRs: 23-45% slower than the 64 x 128 GEMM form, which keeps 33..64 rows).
+// into registers, and v_mfma_f32_32x32x16_bf16 over all 32 tokens.  No LDS staging of weights and
+// no barrier in the main loop: lane l acts as decoder thread (row l % 32 and 32 + l % 32, part
+// l / 32) of each 64-weight step, which is exactly the MFMA's B-operand layout (column l % 32,
+// k-chunk l / 32); its A operand is x of token l % 32 at the same eight k.  One step of weights
+// and x is in flight while the previous one is decoded.  x goes through a 4 KiB LDS region of
+// the wave: read straight in the A layout, every load touched 32 token rows (32 bytes of each
+// 128-byte line), and loaded coalesced (8 whole rows per load) then re-read from LDS the launch
+// is 14-20% faster on gate_up (Q4_K, Q6_K, Q8_0, IQ4_XS at M = 32), 20% on Q6_K down, 3-6% on
+// qkv and the low-bit down shards, even on Q4_K down / o_proj.  Measured against the 32 x 128
+// GEMM tile form it replaced (before the x staging; Q4_K gate_up / qkv / o_proj / down at
+// M = 32: 0.87 / 0.86 / 0.84 / 0.76 of its time; Q2_K, Q8_0, Q6_K down 0.80 / 0.77 / 0.86,
+// IQ4_XS gate_up 0.94; Q6_K and Q8_0 gate_up 1.04).  Tried: weights two steps ahead (more
+// registers, fewer waves: 0-8% slower) and 64 tokens per wave (226-260 VGPRs: 23-45% slower than
+// the 64 x 128 GEMM form, which keeps 33..64 rows).
 template <int T>
-__device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ xr, int kw0,
-                                         int kw1, int c, int r, const GTabs& tb, v16f (&acc)[2]) {
+__device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x, int64_t ldx,
+                                         int M, uint16_t* xl, int kw0, int kw1, int c, int r, const GTabs& tb,
+                                         v16f (&acc)[2]) {
   constexpr int REC = gqk_layout<T>::REC;
   if (kw0 >= kw1) return;
   // k offsets (within a 64-weight step) of the lane's four 8-weight chunks, in MFMA order
   const int koff[4] = {B2<T>::off0(c), B2<T>::off0(c) + 8, B2<T>::off1(c), B2<T>::off1(c) + 8};
   const int s0 = 4 * kw0, last = 4 * kw1 - 1;
-  struct Step { B2<T> w[2]; };
+  // x of a step (32 tokens x 64 k = 32 rows of 128 bytes) comes in with coalesced loads: load i
+  // of lane j takes row 8 i + j / 8, 16-byte chunk (j % 8) ^ swz(row), and the wave writes the four
+  // loads to its LDS region in lane order; the A operand (token l % 32, chunk koff / 8) is then read
+  // at slot chunk ^ swz(token).  swz(t) = (t >> 1) & 7 puts the 16 rows a quarter-wave reads in 16
+  // distinct 16-byte bank groups.
+  const int lane = threadIdx.x & 63;
+  const uint16_t* xsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 8 * i + (lane >> 3);
+    xsrc[i] = x + (int64_t)min(t, M - 1) * ldx + 8 * ((lane & 7) ^ ((t >> 1) & 7));
+  }
+  const int rs = (r >> 1) & 7;
+  struct Step { B2<T> w[2]; v4u xg[4]; };
   Step p0, p1;
   auto load = [&](Step& p, int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.xg[i] = *(const v4u*)(xsrc[i] + (int64_t)s * 64);
     const uint8_t* rc = tbase + (int64_t)(s >> 2) * (64 * REC);
     p.w[0].load(rc, r, s & 3, c);
     p.w[1].load(rc, 32 + r, s & 3, c);
   };
   auto compute = [&](const Step& p, int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ((v4u*)xl)[64 * i + lane] = p.xg[i];
     v8bf a[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) a[q] = *(const v8bf*)(xr + (int64_t)s * 64 + koff[q]);
+    for (int q = 0; q < 4; ++q) a[q] = *(const v8bf*)(xl + (r * 8 + ((koff[q] >> 3) ^ rs)) * 8);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const GS st = p.w[b].prep(s & 3, c);
@@ -903,6 +925,7 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
                                                        int* __restrict__ ctr) {
   constexpr int MP = 32;   // tokens of the plan (partial slots [slot][64 rows][MP])
   __shared__ __attribute__((aligned(16))) uint8_t lds[MID_RED_BYTES + GB_TAB_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t xlds[4 * 2048];   // a 4 KiB x step per wave
   const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
   const int type = dsc[D_TYPE];
   // the wave index is uniform: as an SGPR its k-range, addresses and branches stay scalar (Q6_K,
@@ -932,7 +955,7 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
   const int64_t tile = dsc[D_TILE0];
   const int nb = dsc[D_NB], kb0 = dsc[D_KB0], nk = dsc[D_KB1] - kb0;
   const int kw0 = kb0 + (wave * nk) / nw, kw1 = kb0 + ((wave + 1) * nk) / nw;
-  const uint16_t* xr = x + (int64_t)min(r, M - 1) * ldx;   // tokens past M: clamped, never stored
+  uint16_t* xl = xlds + wave * 2048;
   v16f acc[2];
 #pragma unroll
   for (int b = 0; b < 2; ++b)
@@ -940,7 +963,7 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
     for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
 #define RUN(T)                                                                                                 \
   if ((ONLY == 0 || ONLY == T) && type == T)                                                                   \
-    mid_wave<T>(packed + off + tile * nb * (int64_t)(64 * gqk_layout<T>::REC), xr, kw0, kw1, c, r, tb, acc);
+    mid_wave<T>(packed + off + tile * nb * (int64_t)(64 * gqk_layout<T>::REC), x, ldx, M, xl, kw0, kw1, c, r, tb, acc);
   RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
   RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
 #undef RUN
