@@ -348,8 +348,9 @@ __device__ __forceinline__ void q6_convert(uint8_t* raw, int tid) {
 }
 
 // The 64 raw records of a chunk from its plane-major words (16-byte loads), into raw[row][REC] in
-// LDS (Q6_K's six-bit values converted back to ql / qh before the function returns).
-template <int T>
+// LDS (Q6_K's six-bit values converted back to ql / qh before the function returns, unless
+// Q6_PACKED: then its first 192 bytes stay in the re-packed order).
+template <int T, bool Q6_PACKED = false>
 __device__ __forceinline__ void chunk_to_raw(const uint4* __restrict__ in, uint8_t* raw, int tid) {
   constexpr int REC = gqk_planes<T>::v.rec;
   auto scatter = [&](int wi, auto&& at) {
@@ -363,9 +364,31 @@ __device__ __forceinline__ void chunk_to_raw(const uint4* __restrict__ in, uint8
     }
   };
   every_plane_word<T>(tid, scatter);
-  if constexpr (T == GQK_Q6_K) {
+  if constexpr (T == GQK_Q6_K && !Q6_PACKED) {
     __syncthreads();
     q6_convert<false>(raw, tid);
+  }
+}
+
+// deq32<Q6_K> on a record whose six-bit values are in the re-packed order (gqk_q6_pos): the same
+// weights and the same fp32 bits, without restoring ql / qh first.
+__device__ __forceinline__ void deq32_q6_packed(const uint8_t* rec, int g, float* w) {
+  const float d = f16_at(rec + 208);
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int g16 = 2 * g + hf;
+    const float dl = d * (float)(int8_t)rec[192 + g16];
+    uint32_t top[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 3; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = rec[gqk_q6_pos(g16, m, i)];
+        w[16 * hf + 4 * m + i] = dl * (float)((int)(b & 63) - 32);
+        top[i] |= (b >> 6) << (2 * m);
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[16 * hf + 12 + i] = dl * (float)((int)top[i] - 32);
   }
 }
 
@@ -471,14 +494,15 @@ __global__ __launch_bounds__(256) void tile_dequant_kernel(const uint8_t* __rest
   __shared__ __attribute__((aligned(16))) uint8_t raw[CB + 16];
   const int tid = threadIdx.x;
   const int64_t chunk = blockIdx.x, kb = chunk % nb, tile = chunk / nb;
-  chunk_to_raw<T>((const uint4*)(tiles + chunk * CB), raw, tid);
+  chunk_to_raw<T, true>((const uint4*)(tiles + chunk * CB), raw, tid);
   __syncthreads();
   for (int it = tid; it < 64 * 8; it += 256) {   // consecutive threads: consecutive groups of a row
     const int r = it >> 3, g = it & 7;
     const int64_t row = tile * 64 + r;
     if (row >= n) continue;
     float w[32];
-    deq32<T>(raw + r * REC, g, w);
+    if constexpr (T == GQK_Q6_K) deq32_q6_packed(raw + r * REC, g, w);
+    else deq32<T>(raw + r * REC, g, w);
     O* o = out + row * ldo + kb * 256 + g * 32;
     if constexpr (VEC) {
       constexpr int PER = 16 / sizeof(O);
