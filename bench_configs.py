@@ -98,8 +98,10 @@ def config4(torch, gguf_hip, random_shard, dev, ms: list[int]) -> None:
                 t = _median_ms(g, torch, len(gls), reps=2)
                 del g
                 tf = 2.0 * M * N * K / (t * 1e-3) / 1e12
+                path = "dequant_vendor_gemm" if M >= gguf_hip.ops.DEQUANT_MIN_M else "fused_gemm"
                 _emit({"config": 4, "type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "M": M,
-                       "ms": round(t, 4), "TFLOPs": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
+                       "path": path, "ms": round(t, 4), "TFLOPs": round(tf, 1),
+                       "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4)})
                 del x
             del gls
             torch.cuda.empty_cache()

@@ -38,6 +38,20 @@ GEMV_BUCKETS = (4, 8, 16, 32)
 # GEMM plans: 64 x 128 tiles (33..64 rows), 128 x 128 (65..128), 129..384, 385..512 and 513..768
 # (256 x 256, or 128 x 128 for a layer with few 256-row groups), 256 x 256 above
 GEMM_PLAN_M = (64, 128, 384, 512, 768, 769)
+# From this many batch rows mul_mat_grouped takes the reference's dequant regime (its
+# gluon_mul_mat_tiles_grouped dequantizes the tiles and runs the vendor bf16 GEMM above 128 rows
+# for the types its wide form loses on, gguf-plugin/gluon/interface.py:181-187): each shard is
+# decoded once by the tile dequant kernel and multiplied by torch's bf16 GEMM (hipBLASLt) in row
+# chunks.  Measured on the gate_up / down shards against the fused GEMM: at 8192 rows 12-44%
+# faster on gate_up for Q4_K, Q5_K, Q6_K, IQ4_XS and IQ3_S and, chunked, on `down`; at 4096 rows
+# 4-16%; at 2048 rows from even (Q4_K gate_up, the bench's line) to 12%, so the fused kernel keeps
+# those.  The chunk: DEQUANT_CHUNK_M rows, or DEQUANT_CHUNK_M_LONG_K for K above
+# DEQUANT_LONG_K - the vendor GEMM's 8192-row `down` (K = 17408) ran 2.5x its 4096-row time,
+# while gate_up (K = 5120) in two 4096-row chunks took 1.15x its one 8192-row call.
+DEQUANT_MIN_M = 4096
+DEQUANT_CHUNK_M = 8192
+DEQUANT_LONG_K = 8192
+DEQUANT_CHUNK_M_LONG_K = 4096
 
 _DTYPES = {torch.float32: _lib.GQK_DTYPE_F32, torch.bfloat16: _lib.GQK_DTYPE_BF16, torch.float16: _lib.GQK_DTYPE_F16}
 
@@ -343,7 +357,8 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
     into, for bf16 x; it is returned.  workspace: a zero-filled int32 buffer of at least
     ``gqk_workspace_bytes_max()`` bytes to use instead of the device's shared one (calls that may
     overlap in time on different streams each need their own).  Nothing is allocated here
-    besides the output."""
+    besides the output, below DEQUANT_MIN_M rows; from there the regime is the reference's
+    dequantize + vendor GEMM (a shard's bf16 weights live for the duration of its GEMMs)."""
     _require_gpu(x, "mul_mat_grouped")
     if x.dim() != 2 or x.shape[1] != gl.K:
         raise ValueError(f"mul_mat_grouped: x {tuple(x.shape)} does not match K={gl.K}")
@@ -362,15 +377,44 @@ def mul_mat_grouped(x: torch.Tensor, gl: GroupedLayer, bias: torch.Tensor | None
                 or out.device != x.device or (out.numel() and out.stride(1) != 1)):
             raise ValueError(f"mul_mat_grouped: out must be a bf16 [{xb.shape[0]}, {gl.n_total}] view with unit "
                              f"column stride on {x.device}, for bf16 x")
-        fused_mul_mat_gguf_grouped_out(xb, gl.packed, gl.descs, gl.plans, ws, out, fused)
+        if xb.shape[0] >= DEQUANT_MIN_M:
+            _dequant_mm_into(xb, gl, out)
+            fused = None
+        else:
+            fused_mul_mat_gguf_grouped_out(xb, gl.packed, gl.descs, gl.plans, ws, out, fused)
         if bias is not None and fused is None:
             out.add_(bias)
         return out
-    y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, ws, fused)
+    if xb.shape[0] >= DEQUANT_MIN_M:
+        y = torch.empty((xb.shape[0], gl.n_total), dtype=torch.bfloat16, device=x.device)
+        _dequant_mm_into(xb, gl, y)
+        fused = None
+    else:
+        y = fused_mul_mat_gguf_grouped(xb, gl.packed, gl.descs, gl.plans, gl.n_total, ws, fused)
     y = y if x.dtype == torch.bfloat16 else y.to(x.dtype)
     if bias is not None and fused is None:
         y.add_(bias)
     return y
+
+
+def _dequant_mm_into(xb: torch.Tensor, gl: GroupedLayer, y: torch.Tensor) -> None:
+    """The dequant regime (DEQUANT_MIN_M rows and more): each shard's weights decoded from its
+    tiles to bf16 (the same bits as the fused kernels' decode) and multiplied by torch's bf16 GEMM
+    in row chunks, into the shard's columns of y.  Allocates the shard's bf16 weights for the
+    duration of its GEMMs."""
+    col = 0
+    chunk = DEQUANT_CHUNK_M_LONG_K if gl.K > DEQUANT_LONG_K else DEQUANT_CHUNK_M
+    for view, n, wt in zip(gl.views, gl.n_outs, gl.weight_types):
+        w = dequantize_tiles(view, n, gl.K, wt, torch.bfloat16)
+        for r0 in range(0, xb.shape[0], chunk):
+            r1 = min(xb.shape[0], r0 + chunk)
+            ys = y[r0:r1, col:col + n]
+            if ys.is_contiguous():
+                torch.mm(xb[r0:r1], w.t(), out=ys)
+            else:
+                ys.copy_(torch.mm(xb[r0:r1], w.t()))
+        del w
+        col += n
 
 
 _CACHE_ATTR = "_gguf_hip_layers"

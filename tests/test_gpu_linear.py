@@ -538,3 +538,41 @@ def test_mid_form_17_to_32_rows(dev, wt):
             assert bool((wide[:, 24 + n:] == 7).all()), (target, M)
         torch.cuda.synchronize()
         assert int(gl.workspace[:info.ctr_bytes // 4].abs().sum()) == 0
+
+
+def test_dequant_regime_large_m(dev, monkeypatch):
+    """From DEQUANT_MIN_M rows mul_mat_grouped takes the reference's dequant regime (each shard's
+    tiles dequantized, the vendor bf16 GEMM in row chunks): a mixed layer, with a bias and into a
+    column slice of a wider output, matches the oracle on both sides of the threshold and at a
+    chunk remainder; and at the default threshold a small layer at 4096 rows does too."""
+    import gguf_hip
+    from gguf_hip import ops
+
+    rng = np.random.default_rng(21)
+    K = 1536
+    shards = [(G.Q4_K, 128), (G.Q6_K, 100), (G.IQ3_S, 70)]
+    raws = [G.make_weights(rng, n, K, wt) for wt, n in shards]
+    wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
+    gl = gguf_hip.pack_layer([torch.from_numpy(r).to(dev) for r in raws], [n for _, n in shards],
+                             [wt for wt, _ in shards])
+    n_total = sum(n for _, n in shards)
+    bias = (torch.randn(n_total, device=dev) * 4).to(torch.bfloat16)
+    monkeypatch.setattr(ops, "DEQUANT_MIN_M", 48)
+    monkeypatch.setattr(ops, "DEQUANT_CHUNK_M", 40)
+    monkeypatch.setattr(ops, "DEQUANT_CHUNK_M_LONG_K", 40)
+    for M in (47, 48, 100):
+        x = _x(M, K, 8000 + M, dev)
+        ref = _ref(x, wf)
+        assert G.rel_err(gguf_hip.mul_mat_grouped(x, gl).float().cpu().numpy(), ref) < TOL, M
+        yb = gguf_hip.mul_mat_grouped(x, gl, bias).float().cpu().numpy()
+        assert G.rel_err(yb, ref + bias.float().cpu().numpy()[None]) < TOL, M
+        wide = torch.full((M, n_total + 24), 7.0, dtype=torch.bfloat16, device=dev)
+        gguf_hip.mul_mat_grouped(x, gl, out=wide[:, 8:8 + n_total])
+        assert G.rel_err(wide[:, 8:8 + n_total].float().cpu().numpy(), ref) < TOL, M
+        assert bool((wide[:, :8] == 7).all()) and bool((wide[:, 8 + n_total:] == 7).all()), M
+    monkeypatch.undo()
+    assert ops.DEQUANT_MIN_M == 4096
+    raw = G.make_weights(rng, 96, 512, G.Q4_K)
+    gl1 = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [96], [G.Q4_K])
+    x = _x(4096, 512, 8100, dev)
+    assert G.rel_err(gguf_hip.mul_mat_grouped(x, gl1).float().cpu().numpy(), _ref(x, G.dequantize(raw, G.Q4_K))) < TOL
