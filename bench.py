@@ -20,6 +20,7 @@ torch.matmul in fp32) on a bounded row sample of the Q4_K / Q6_K gate_up shards.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -169,6 +170,8 @@ def main() -> int:
     ap.add_argument("--stack-layers", type=int, default=64, help="config 5 lines: decoder layers (0: skip)")
     ap.add_argument("--gemm-m", type=int, default=2048, help="batch rows of the prefill GEMM line (0: skip)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-floor", dest="floor", action="store_false",
+                    help="skip the per-shard memory floor (plain streaming read of the same bytes)")
     ap.add_argument("--detail", action="store_true", help="print the per-shard table to stderr")
     ap.add_argument("--only", default="", help="TYPE:SHARD (e.g. Q6_K:gate_up): run that shard alone, "
                     "so a profiler's per-kernel statistics cover exactly one launch shape")
@@ -250,6 +253,25 @@ def main() -> int:
         del g
         return t * 1e3
 
+    # the shard's memory floor: a plain streaming read of the same packed bytes on the shard's own
+    # grid (gqk_read_floor), timed the same way (the same rotating copies, graph replays, events)
+    def floor_us(gls, grid, waves):
+        sink = torch.empty(grid * waves, dtype=torch.int32, device=dev)
+        reps = max(1, 8 // len(gls))
+
+        def f():
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for _ in range(reps):
+                for gl in gls:
+                    gguf_hip._lib.check(gguf_hip._lib.lib.gqk_read_floor(
+                        gl.packed.data_ptr(), gl.packed.numel() // 1024 * 1024, grid, waves, sink.data_ptr(), st),
+                        "read_floor")
+        g = _capture(f, torch)
+        g.replay()
+        t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (reps * len(gls))
+        del g
+        return t * 1e3
+
     def plan_of(gl, m):
         return gguf_hip.ops.GqkPlanInfo.from_tuple(
             gl.plans[gguf_hip.ops._pick_plan(gl.plans, m) * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
@@ -258,10 +280,12 @@ def main() -> int:
     for wt, name, N, K, gls, nb in shards:
         us = shard_us(gls, xs[K])
         info = plan_of(gls[0], M)
+        fl = floor_us(gls, info.n_desc, info.nw) if args.floor else None
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
                      "copies": len(gls),
                      "GBps": round(nb / (us * 1e-6) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
-                     "waves_per_wg": info.nw, "one_record": info.bm == 1})
+                     "waves_per_wg": info.nw, "one_record": info.bm == 1,
+                     "floor_us": round(fl, 2) if fl else None})
     # the rest of the metric's range (M = 9..32: speculative rows of several streams)
     extra = []
     for Me in [int(v) for v in args.extra_m.split(",") if v]:
@@ -348,6 +372,14 @@ def main() -> int:
                      "kernel": f"{dom['type']} {dom['shard']} {dom['N']}x{dom['K']} M={M}", "symbol": dom_symbol,
                      "launch_us": dom["us"], "bytes_per_launch": dom_bytes},
         "shards": rows,
+        "memory_floor": None if not args.floor else {
+            "what": "gqk_read_floor: a plain streaming read of each shard's packed bytes on the shard's own grid "
+                    "(same rotating copies, graph replays and events as the shard lines); the sum over the "
+                    "step's shards against the sum of their launch times",
+            "floor_us": round(sum(r["floor_us"] for r in rows), 2),
+            "launch_us": round(sum(r["us"] for r in rows), 2),
+            "floor_GBps": round(step_bytes / (sum(r["floor_us"] for r in rows) * 1e-6) / 1e9, 1),
+            "frac_of_floor": round(sum(r["floor_us"] for r in rows) / sum(r["us"] for r in rows), 4)},
         "shards_extra_m": extra,
         "gemm": gemm,
         "stack": stack,

@@ -93,6 +93,33 @@ int scratch_for_current_device(hipStream_t st, void** out) {
   return GQK_OK;
 }
 
+// The memory floor of a shard: a plain streaming read of its packed bytes on a given grid.  Wave
+// w of W reads the 1 KiB units [w n / W, (w + 1) n / W) of the buffer, kFloorLoads units (one
+// 16-byte buffer load per lane each) in flight per step, and folds them into one word per wave so
+// the loads stay live.  Units past the wave's range read out of the buffer's bounds (zeros,
+// no memory access).
+constexpr int kFloorLoads = 16;
+typedef uint32_t v4u_fl __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) void read_floor_kernel(const uint8_t* buf, uint32_t units,
+                                                                           uint32_t* sink) {
+  const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+  const uint64_t W = (uint64_t)gridDim.x * nw, w = (uint64_t)blockIdx.x * nw + (threadIdx.x >> 6);
+  const uint32_t u0 = (uint32_t)(w * units / W), u1 = (uint32_t)((w + 1) * units / W);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)buf, 0, units * 1024u, 0x00020000);
+  uint32_t acc = 0;
+  for (uint32_t u = u0; u < u1; u += kFloorLoads) {
+    v4u_fl v[kFloorLoads];
+#pragma unroll
+    for (int i = 0; i < kFloorLoads; ++i)
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, u + i < u1 ? (u + i) * 1024u + lane * 16u : 0xFFFFFFF0u, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kFloorLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+  }
+  for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+  if (lane == 0) sink[w] = acc;
+}
+
 }  // namespace
 
 void gqk_set_last_error(const char* msg) { g_err = msg ? msg : ""; }
@@ -483,6 +510,17 @@ int gqk_linear_noalloc(const void* packed, const int32_t* desc_dev, const gqk_pl
   if (rc) return rc;
   return gqk_linear(packed, desc_dev, info, x, ldx, M, y, ldy, bias, need > 0 ? ws : nullptr, need > 0 ? kScratchBytes : 0,
                     stream);
+}
+
+int gqk_read_floor(const void* buf, int64_t bytes, int grid, int waves, void* sink, void* stream) {
+  if (!buf || !sink) return fail(GQK_ERR_ARG, "read_floor: null pointer");
+  if (bytes < 1024 || bytes % 1024 || bytes > ((int64_t)1 << 31))
+    return fail(GQK_ERR_SHAPE, "read_floor: %lld bytes (a multiple of 1 KiB, at most 2 GiB)", (long long)bytes);
+  if (grid < 1 || waves < 1 || waves > GQK_GEMV_MAX_WAVES)
+    return fail(GQK_ERR_SHAPE, "read_floor: grid %d x %d waves (1..%d waves)", grid, waves, GQK_GEMV_MAX_WAVES);
+  hipLaunchKernelGGL(read_floor_kernel, dim3(grid), dim3(64 * waves), 0, (hipStream_t)stream, (const uint8_t*)buf,
+                     (uint32_t)(bytes / 1024), (uint32_t*)sink);
+  return check_launch("read_floor");
 }
 
 }  // extern "C"

@@ -27,7 +27,7 @@ EXPORTS = ("gqk_last_error", "gqk_version", "gqk_type_info", "gqk_dequantize", "
            "gqk_tiles_bytes", "gqk_repack", "gqk_unrepack", "gqk_plan", "gqk_linear_workspace_bytes",
            "gqk_workspace_bytes_max", "gqk_linear", "gqk_linear_noalloc", "gqk_ggml_type_size",
            "gqk_gguf_open", "gqk_gguf_close", "gqk_gguf_info", "gqk_gguf_tensor_at", "gqk_gguf_find_tensor",
-           "gqk_gguf_kv_at", "gqk_gguf_find_kv", "gqk_gguf_kv_string", "gqk_gguf_upload_tiles")
+           "gqk_gguf_kv_at", "gqk_gguf_find_kv", "gqk_gguf_kv_string", "gqk_gguf_upload_tiles", "gqk_read_floor")
 
 
 class GqkShard(ctypes.Structure):
@@ -103,6 +103,7 @@ def _load() -> ctypes.CDLL:
         "gqk_gguf_find_kv": (i64, [vp, ctypes.c_char_p]),
         "gqk_gguf_kv_string": (i32, [vp, i64, i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_int64)]),
         "gqk_gguf_upload_tiles": (i32, [vp, i64, vp, i64, vp, vp]),
+        "gqk_read_floor": (i32, [vp, i64, i32, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

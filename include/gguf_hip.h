@@ -125,6 +125,13 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
  * partials are transient torch tensors (gguf-plugin/gluon/tiles_grouped.py:1233-1238). */
 int64_t gqk_workspace_bytes_max(void);
 
+/* Measurement only, no counterpart in the reference: a plain streaming read of `bytes` (a
+ * multiple of 1 KiB, at most 2 GiB) at `buf` on `grid` workgroups of `waves` (1..8) waves, each
+ * wave reading one contiguous share and writing one folded word to sink[wave] (grid * waves
+ * uint32 words).  Timed over a shard's packed bytes on the shard's own grid it gives the memory
+ * floor that bench.py reports beside each launch. */
+int gqk_read_floor(const void* buf, int64_t bytes, int grid, int waves, void* sink, void* stream);
+
 /* y[M, ldy] (bf16) = x[M, ldx] (bf16) @ W^T (+ bias) over the grouped layer's shards (columns in
  * shard order), on `stream`.  bias: NULL or bf16 [info->n_total] device memory, added in fp32
  * before the single rounding to bf16 (the reference adds it afterwards with out.add_(bias),

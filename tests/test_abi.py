@@ -129,6 +129,21 @@ def _check_gemv_rows(shards, K, info, desc):
     return ncs
 
 
+def test_read_floor_argument_checks():
+    """The measurement-only plain read refuses null buffers, sizes that are not whole KiB (or
+    beyond 2 GiB) and grids outside 1..8 waves before any launch."""
+    from gguf_hip import _lib
+
+    f = _lib.lib.gqk_read_floor
+    assert f(None, 1024, 1, 1, None, None) == _lib.GQK_ERR_ARG
+    p = ctypes.c_void_p(4096)                      # never dereferenced: the checks come first
+    assert f(p, 1000, 1, 1, p, None) == _lib.GQK_ERR_SHAPE
+    assert f(p, (1 << 31) + 1024, 1, 1, p, None) == _lib.GQK_ERR_SHAPE
+    assert f(p, 1024, 0, 1, p, None) == _lib.GQK_ERR_SHAPE
+    assert f(p, 1024, 1, 9, p, None) == _lib.GQK_ERR_SHAPE
+    assert "read_floor" in _lib.lib.gqk_last_error().decode()
+
+
 def test_plan_gemv_balanced_split_partition():
     from gguf_hip import _lib, ops
 

@@ -260,3 +260,28 @@ def test_graph_then_larger_eager_call_then_replay(dev):
         assert torch.equal(y, eager), M
     assert gla.workspace.data_ptr() == ws_ptr and glb.workspace is gla.workspace
     assert G.rel_err(y.float().cpu().numpy(), _ref(x8, G.dequantize(raw_a, G.Q4_K))) < TOL
+
+
+def test_read_floor_reads_every_byte(dev):
+    """bench.py's memory floor reads each byte of the buffer once: every wave's folded word is the
+    XOR of all 32-bit words of its contiguous share of 1 KiB units (a ragged split: 1,000 units
+    over 7 x 3 waves, and one wave over everything)."""
+    import ctypes
+
+    from gguf_hip import _lib
+
+    n_units = 1000
+    g = torch.Generator().manual_seed(7)
+    words = torch.randint(-2**31, 2**31 - 1, (n_units * 256,), generator=g, dtype=torch.int64).to(torch.int32)
+    buf = words.to(dev)
+    unit_xor = np.bitwise_xor.reduce(words.numpy().view(np.uint32).reshape(n_units, 256), axis=1)
+    for grid, waves in ((7, 3), (1, 1)):
+        W = grid * waves
+        sink = torch.zeros(W, dtype=torch.int32, device=dev)
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        assert _lib.lib.gqk_read_floor(buf.data_ptr(), n_units * 1024, grid, waves, sink.data_ptr(), st) == 0
+        torch.cuda.synchronize()
+        got = sink.cpu().numpy().view(np.uint32)
+        want = np.array([np.bitwise_xor.reduce(unit_xor[w * n_units // W:(w + 1) * n_units // W]) for w in range(W)],
+                        dtype=np.uint32)
+        assert np.array_equal(got, want)
