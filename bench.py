@@ -63,6 +63,13 @@ def _capture(fn, torch):
     return g
 
 
+def _form(info) -> str:
+    """The launch form of a plan: the GEMV (token groups g), its slab form, the mid form, the GEMM tile."""
+    if info.form != 1:
+        return f"gemm{info.bm}"
+    return f"slab_g{info.g}" if info.bm == 2 else f"gemv_g{info.g}" if info.g <= 4 else "mid"
+
+
 def _source_sha16(rel: str) -> str:
     import hashlib
 
@@ -265,7 +272,7 @@ def main() -> int:
                 for gl in gls:
                     gguf_hip._lib.check(gguf_hip._lib.lib.gqk_read_floor(
                         gl.packed.data_ptr(), gl.packed.numel() // 1024 * 1024, grid, waves, sink.data_ptr(), st),
-                        "read_floor")
+                        "bench floor")
         g = _capture(f, torch)
         g.replay()
         t = statistics.median(_time_graph(g, 5, torch) for _ in range(5)) / (reps * len(gls))
@@ -284,7 +291,7 @@ def main() -> int:
         rows.append({"type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
                      "copies": len(gls),
                      "GBps": round(nb / (us * 1e-6) / 1e9, 1), "g": info.g, "split": info.split, "wgs": info.n_desc,
-                     "waves_per_wg": info.nw, "one_record": info.bm == 1,
+                     "waves_per_wg": info.nw, "one_record": info.bm == 1, "form": _form(info),
                      "floor_us": round(fl, 2) if fl else None})
     # the rest of the metric's range (M = 9..32: speculative rows of several streams)
     extra = []
@@ -295,7 +302,7 @@ def main() -> int:
             info = plan_of(gls[0], Me)
             gbs = nb / (us * 1e-6) / 1e9
             extra.append({"M": Me, "type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "us": round(us, 2),
-                          "form": (f"gemv_g{info.g}" if info.g <= 4 else "mid") if info.form == 1 else f"gemm{info.bm}", "GBps": round(gbs, 1),
+                          "form": _form(info), "GBps": round(gbs, 1),
                           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
         del xe
     dom = max(rows, key=lambda r: r["us"])

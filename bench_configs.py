@@ -70,7 +70,8 @@ def config3(torch, gguf_hip, random_shard, dev, ms: list[int], types=ALL_TYPES, 
                 gbs = nbytes / (t * 1e-3) / 1e9
                 i = gguf_hip.ops._pick_plan(gls[0].plans, M)
                 info = gguf_hip.ops.GqkPlanInfo.from_tuple(gls[0].plans[i * gguf_hip.ops._NPLAN:][:gguf_hip.ops._NPLAN])
-                form = (f"gemv_g{info.g}" if info.g <= 4 else "mid") if info.form == 1 else f"gemm{info.bm}"
+                form = (("slab_g%d" % info.g if info.bm == 2 else f"gemv_g{info.g}") if info.g <= 4 else "mid") \
+                    if info.form == 1 else f"gemm{info.bm}"
                 _emit({"config": 3, "type": gguf_hip.TYPE_NAMES[wt], "shard": name, "N": N, "K": K, "M": M,
                        "form": form, "us": round(t * 1e3, 2), "packed_bytes": nbytes,
                        "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "copies": len(gls)})

@@ -101,7 +101,7 @@ int scratch_for_current_device(hipStream_t st, void** out) {
 constexpr int kFloorLoads = 16;
 typedef uint32_t v4u_fl __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(64 * GQK_GEMV_MAX_WAVES) void read_floor_kernel(const uint8_t* buf, uint32_t units,
+__global__ __launch_bounds__(1024) void read_floor_kernel(const uint8_t* buf, uint32_t units,
                                                                            uint32_t* sink) {
   const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
   const uint64_t W = (uint64_t)gridDim.x * nw, w = (uint64_t)blockIdx.x * nw + (threadIdx.x >> 6);
@@ -283,83 +283,115 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     pi.form = GQK_FORM_GEMV;
     pi.g = M <= 4 ? 1 : M <= 8 ? 2 : M <= 16 ? 4 : 8;
     pi.m_max = 4 * pi.g;
-    // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
-    // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
-    // workgroup holds does K split across workgroups.  Every wave keeps >= 1 super-block.
-    // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
-    // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
-    // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
-    int64_t target = target_wgs > 0 ? target_wgs : (int64_t)kWavesPerCu * cus;
-    // Up to four rows (one token group), when every wave can hold exactly one record (k-range a
-    // multiple of four super-blocks, at most GQK_SPLIT_MAX workgroups per tile): one record per
-    // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances
-    // the CUs, which beats streaming waves there (gate_up 34816 x 5120 at M = 1: Q6_K 34.9 -> 32.5
-    // us, Q5_K 31.4 -> 28.7, IQ4_XS 30.6 -> 29.1, Q5_0 31.4 -> 28.3; the others within 1 us); at 8 rows
-    // the heavier per-record work makes the streaming plan the faster one for a single type.  A
-    // mixed-type layer takes it up to eight rows: its streaming kernel holds the registers of its
-    // costliest format (~235 VGPRs: two waves per SIMD) where the one-record kernel needs ~100
-    // (a mixed stack's qkv + o_proj + gate_up launches at K = 5120, M = 8: 49.0 -> 43.2 us per layer; at 16
-    // rows no gain, and splitting `down`'s 68 super-blocks 17 ways measured no better either).
-    if (target_wgs <= 0 && (pi.g == 1 || (mixed && pi.g == 2)) && nb % kGemvWaves == 0 &&
-        nb / kGemvWaves <= GQK_SPLIT_MAX)
-      target = tiles * nb;
-    const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
-    const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
-    const int64_t split =
-        std::max<int64_t>(1, std::min({(per_tile + nw - 1) / nw, nb / nw, (int64_t)GQK_SPLIT_MAX}));
-    // Tail: with whole tiles (split 1) in more than one round of resident workgroups (target / nw
-    // of them, two per CU at the default target), a last round of r <= half the slots would put
-    // a third whole tile on r CUs, which then finish last (gate_up's 544 tiles on 256 CUs: 28.5 us
-    // against 22.2 us for 512).  Those r tiles split K instead, into workgroups of >= one record a
-    // wave, so their work spreads over up to half the CUs as light extra workgroups.
-    const int64_t slots = std::max<int64_t>(1, target / nw);
-    int64_t tail = 0, split_tail = 1;
-    if (split == 1 && tiles > slots) {
-      const int64_t r = tiles % slots;
-      if (r > 0 && 2 * r <= slots) split_tail = std::min<int64_t>({nb / nw, std::max<int64_t>(1, slots / 2 / r),
-                                                                   (int64_t)GQK_SPLIT_MAX});
-      if (split_tail > 1) tail = r;
-    }
-    pi.nw = (int32_t)nw;
-    pi.split = (int32_t)std::max(split, split_tail);
-    // One round of split tiles whose waves stream >= 2 records each: fill the resident slots
-    // exactly (s0 or s0 + 1 rows per tile) rather than overshoot them and leave a few CUs a third
-    // workgroup (down 5120 x 17408: 560 -> 512 workgroups, Q6_K M = 1 26.0 -> 21.3 us).  With one
-    // record per wave (qkv, o_proj at K = 5120) the extra workgroups' memory parallelism wins.
-    int64_t s0 = split, extra = 0;
-    if (split > 1 && tiles <= slots && nb >= 2 * split * nw) {
-      const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(nb / nw, GQK_SPLIT_MAX));
-      const int64_t total = std::min(slots, tiles * smax);
-      s0 = std::max<int64_t>(1, total / tiles);
-      extra = s0 < smax ? total - s0 * tiles : 0;
-      pi.split = (int32_t)(s0 + (extra > 0));
-    }
-    int64_t col0 = 0, g = 0, ctr = 0, slot = 0;
-    bool one_record = true;   // every wave of every row streams exactly one record
+    // The slab form (up to 8 rows): a workgroup per 32-row half of a tile over the whole k-range,
+    // one wave per pair of super-blocks, each staging its own x in LDS; no split-K exchange.  One
+    // workgroup per CU, so its time follows the slab's bytes, not the shard's: taken when the
+    // slabs fill one round of the CUs, at least half of them up to 4 rows and three quarters up
+    // to 8.  Measured on 256 CUs against the split-K plans (eight types, µs): qkv 7168 x 5120
+    // (224 slabs) 0.3-1.7 faster at M = 1 / 4 and 0.2-1.5 at M = 8; o_proj 5120 x 5120 (160 slabs)
+    // 0.3-0.6 faster at M = 1 / 4, but at M = 8 even to 0.7 slower (Q4_K 9.1 -> 9.8).
+    int64_t slabs = 0;
+    bool any_iq = false;
     for (int i = 0; i < nshards; ++i) {
-      int64_t ntile = (shards[i].n + 63) / 64;
-      for (int64_t t0 = 0; t0 < ntile; ++t0, ++g) {
-        const int64_t sp = g >= tiles - tail ? split_tail : split > 1 ? s0 + (g < extra) : split;
-        if (sp == 1) {
-          row(i, t0, 1, 0, nb, 0, col0, 0);
-          one_record &= nb == nw;
-          continue;
-        }
-        for (int64_t s = 0; s < sp; ++s) {   // balanced partition: every split owns >= 1 super-block
-          row(i, t0, 1, s * nb / sp, (s + 1) * nb / sp, (int)s, col0, ctr, (int)sp, slot);
-          one_record &= (s + 1) * nb / sp - s * nb / sp == nw;
-        }
-        ++ctr;
-        slot += sp;
-      }
-      col0 += shards[i].n;
+      const int64_t rem = shards[i].n % 64;
+      slabs += 2 * ((shards[i].n + 63) / 64) - (rem != 0 && rem <= 32 ? 1 : 0);
+      const int t = shards[i].ggml_type;
+      any_iq |= t == GQK_IQ4_NL || t == GQK_IQ4_XS || t == GQK_IQ3_S;
     }
-    // a plan whose waves all hold a single record launches the kernel built without the register
-    // pipeline (fewer registers: more workgroups resident), flagged in the GEMM-only bm field
-    pi.bm = one_record && pi.g <= 4 ? 1 : 0;
-    // workspace: the counter region (one arrival counter per split tile; zero before the first
-    // launch, left zero by each launch), then the fp32 partial slots [slot][64 rows][m_max tokens]
-    pi.workspace_bytes = slot > 0 ? ctr_bytes + gqk_partial_bytes(slot, 1, pi.m_max) : 0;
+    const bool slab = target_wgs <= 0 && pi.g <= 2 && nb <= 2 * GQK_SLAB_MAX_WAVES &&
+                      nb * GQK_SLAB_SB_BYTES(pi.m_max) + (any_iq ? GQK_GEMV_TAB_BYTES : 0) <= GQK_SLAB_MAX_LDS &&
+                      (pi.g == 1 ? 2 * slabs >= cus : 4 * slabs >= 3 * (int64_t)cus) && slabs <= cus;
+    if (slab) {
+      pi.bm = GQK_GEMV_SLAB;
+      pi.nw = (int32_t)((nb + 1) / 2);
+      pi.split = 1;
+      int64_t col0 = 0;
+      for (int i = 0; i < nshards; ++i) {
+        const int64_t ntile = (shards[i].n + 63) / 64;
+        for (int64_t t0 = 0; t0 < ntile; ++t0)
+          for (int h = 0; h < 2 && 64 * t0 + 32 * h < shards[i].n; ++h) row(i, t0, 1, 0, nb, h, col0, 0);
+        col0 += shards[i].n;
+      }
+      pi.workspace_bytes = 0;
+    } else {
+      // waves per tile from the wave target; a workgroup's waves (at most nwmax: the x staging of
+      // G >= 4 needs more LDS) split its k-range, and only when a tile wants more waves than one
+      // workgroup holds does K split across workgroups.  Every wave keeps >= 1 super-block.
+      // (Measured: a balanced stream that cuts the records into equal ranges per workgroup, so
+      // that tile counts not a multiple of the CU count leave no tail, ran slower: its shared
+      // tiles' partial exchange and shorter per-wave streams cost more than the tail.)
+      int64_t target = target_wgs > 0 ? target_wgs : (int64_t)kWavesPerCu * cus;
+      // Up to four rows (one token group), when every wave can hold exactly one record (k-range a
+      // multiple of four super-blocks, at most GQK_SPLIT_MAX workgroups per tile): one record per
+      // wave in short-lived workgroups.  Their loads all go out at once and the dispatcher balances
+      // the CUs, which beats streaming waves there (gate_up 34816 x 5120 at M = 1: Q6_K 34.9 -> 32.5
+      // us, Q5_K 31.4 -> 28.7, IQ4_XS 30.6 -> 29.1, Q5_0 31.4 -> 28.3; the others within 1 us); at 8 rows
+      // the heavier per-record work makes the streaming plan the faster one for a single type.  A
+      // mixed-type layer takes it up to eight rows: its streaming kernel holds the registers of its
+      // costliest format (~235 VGPRs: two waves per SIMD) where the one-record kernel needs ~100
+      // (a mixed stack's qkv + o_proj + gate_up launches at K = 5120, M = 8: 49.0 -> 43.2 us per layer; at 16
+      // rows no gain, and splitting `down`'s 68 super-blocks 17 ways measured no better either).
+      if (target_wgs <= 0 && (pi.g == 1 || (mixed && pi.g == 2)) && nb % kGemvWaves == 0 &&
+          nb / kGemvWaves <= GQK_SPLIT_MAX)
+        target = tiles * nb;
+      const int64_t per_tile = std::max<int64_t>(1, (target + tiles - 1) / tiles);
+      const int64_t nw = std::max<int64_t>(1, std::min({per_tile, nb, (int64_t)kGemvWaves}));
+      const int64_t split =
+          std::max<int64_t>(1, std::min({(per_tile + nw - 1) / nw, nb / nw, (int64_t)GQK_SPLIT_MAX}));
+      // Tail: with whole tiles (split 1) in more than one round of resident workgroups (target / nw
+      // of them, two per CU at the default target), a last round of r <= half the slots would put
+      // a third whole tile on r CUs, which then finish last (gate_up's 544 tiles on 256 CUs: 28.5 us
+      // against 22.2 us for 512).  Those r tiles split K instead, into workgroups of >= one record a
+      // wave, so their work spreads over up to half the CUs as light extra workgroups.
+      const int64_t slots = std::max<int64_t>(1, target / nw);
+      int64_t tail = 0, split_tail = 1;
+      if (split == 1 && tiles > slots) {
+        const int64_t r = tiles % slots;
+        if (r > 0 && 2 * r <= slots) split_tail = std::min<int64_t>({nb / nw, std::max<int64_t>(1, slots / 2 / r),
+                                                                     (int64_t)GQK_SPLIT_MAX});
+        if (split_tail > 1) tail = r;
+      }
+      pi.nw = (int32_t)nw;
+      pi.split = (int32_t)std::max(split, split_tail);
+      // One round of split tiles whose waves stream >= 2 records each: fill the resident slots
+      // exactly (s0 or s0 + 1 rows per tile) rather than overshoot them and leave a few CUs a third
+      // workgroup (down 5120 x 17408: 560 -> 512 workgroups, Q6_K M = 1 26.0 -> 21.3 us).  With one
+      // record per wave (qkv, o_proj at K = 5120) the extra workgroups' memory parallelism wins.
+      int64_t s0 = split, extra = 0;
+      if (split > 1 && tiles <= slots && nb >= 2 * split * nw) {
+        const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(nb / nw, GQK_SPLIT_MAX));
+        const int64_t total = std::min(slots, tiles * smax);
+        s0 = std::max<int64_t>(1, total / tiles);
+        extra = s0 < smax ? total - s0 * tiles : 0;
+        pi.split = (int32_t)(s0 + (extra > 0));
+      }
+      int64_t col0 = 0, g = 0, ctr = 0, slot = 0;
+      bool one_record = true;   // every wave of every row streams exactly one record
+      for (int i = 0; i < nshards; ++i) {
+        int64_t ntile = (shards[i].n + 63) / 64;
+        for (int64_t t0 = 0; t0 < ntile; ++t0, ++g) {
+          const int64_t sp = g >= tiles - tail ? split_tail : split > 1 ? s0 + (g < extra) : split;
+          if (sp == 1) {
+            row(i, t0, 1, 0, nb, 0, col0, 0);
+            one_record &= nb == nw;
+            continue;
+          }
+          for (int64_t s = 0; s < sp; ++s) {   // balanced partition: every split owns >= 1 super-block
+            row(i, t0, 1, s * nb / sp, (s + 1) * nb / sp, (int)s, col0, ctr, (int)sp, slot);
+            one_record &= (s + 1) * nb / sp - s * nb / sp == nw;
+          }
+          ++ctr;
+          slot += sp;
+        }
+        col0 += shards[i].n;
+      }
+      // a plan whose waves all hold a single record launches the kernel built without the register
+      // pipeline (fewer registers: more workgroups resident), flagged in the GEMM-only bm field
+      pi.bm = one_record && pi.g <= 4 ? 1 : 0;
+      // workspace: the counter region (one arrival counter per split tile; zero before the first
+      // launch, left zero by each launch), then the fp32 partial slots [slot][64 rows][m_max tokens]
+      pi.workspace_bytes = slot > 0 ? ctr_bytes + gqk_partial_bytes(slot, 1, pi.m_max) : 0;
+    }
   } else {
     pi.form = GQK_FORM_GEMM;
     // 64 / 128 tokens x 128 rows per tile up to 128 tokens (one decode of each weight); 256 x 256 above.
@@ -474,7 +506,7 @@ int gqk_linear(const void* packed, const int32_t* desc_dev, const gqk_plan_info*
       partials = (float*)((char*)workspace + cb);
     }
     int rc = gqk::launch_gemv((const uint8_t*)packed, desc_dev, info->n_desc, info->types_mask, x, ldx, M, info->g, info->nw,
-                              info->bm == 1, y, ldy, bias, partials, counters, (hipStream_t)stream);
+                              info->bm, info->nb, y, ldy, bias, partials, counters, (hipStream_t)stream);
     if (rc) return fail(rc, "linear: GEMV launch form");
     return check_launch("linear (GEMV)");
   }
@@ -516,8 +548,8 @@ int gqk_read_floor(const void* buf, int64_t bytes, int grid, int waves, void* si
   if (!buf || !sink) return fail(GQK_ERR_ARG, "read_floor: null pointer");
   if (bytes < 1024 || bytes % 1024 || bytes > ((int64_t)1 << 31))
     return fail(GQK_ERR_SHAPE, "read_floor: %lld bytes (a multiple of 1 KiB, at most 2 GiB)", (long long)bytes);
-  if (grid < 1 || waves < 1 || waves > GQK_GEMV_MAX_WAVES)
-    return fail(GQK_ERR_SHAPE, "read_floor: grid %d x %d waves (1..%d waves)", grid, waves, GQK_GEMV_MAX_WAVES);
+  if (grid < 1 || waves < 1 || waves > 16)
+    return fail(GQK_ERR_SHAPE, "read_floor: grid %d x %d waves (1..16 waves)", grid, waves);
   hipLaunchKernelGGL(read_floor_kernel, dim3(grid), dim3(64 * waves), 0, (hipStream_t)stream, (const uint8_t*)buf,
                      (uint32_t)(bytes / 1024), (uint32_t*)sink);
   return check_launch("read_floor");

@@ -140,6 +140,11 @@ GQK_LAYOUT(GQK_IQ4_XS, 136, 0, 128)
 #define GQK_CTR_WORDS (GQK_CTR_BYTES / 4)
 #define GQK_GEMV_MAX_M 32   // batch rows of the streaming forms (GEMV up to 16, mid form 17..32); GEMM above
 #define GQK_GEMV_MAX_WAVES 8   // waves per GEMV workgroup (two per SIMD: no register bound below 256)
+#define GQK_GEMV_SLAB 2        // plan bm of the GEMV slab form (M <= 8: a workgroup per 32-row slab, x in LDS)
+#define GQK_SLAB_MAX_WAVES 12  // slab form: waves per workgroup (one per pair of super-blocks: nb <= 24)
+#define GQK_SLAB_MAX_LDS 153600   // slab form: LDS bytes of x (+ the IQ tables) per workgroup
+#define GQK_SLAB_SB_BYTES(mpad) (608 * (mpad))   // LDS bytes of one super-block's staged x (slots + sums)
+#define GQK_GEMV_TAB_BYTES 9216  // LDS bytes of the IQ lookup tables
 enum {
   D_TYPE = 0,     // GGML type of the row's shard
   D_OFF_LO = 1,   // byte offset of the shard's tiles in the packed buffer (low 32 bits)

@@ -382,6 +382,25 @@ __device__ __forceinline__ v4f mfma1_bcast(int ab, float a, float b, v4f c) {
   }
   return c;
 }
+// The same within each half of the wave (CBSZ = 3: blocks 0-7 and 8-15 each take block ab of their
+// own half), for the slab form whose lane halves multiply different super-blocks.
+#define GQK_AB8_CASES(F) F(0) F(1) F(2) F(3) F(4) F(5) F(6) F(7)
+__device__ __forceinline__ v4f mfma4_bcast8(int ab, v4s a, v4s b, v4f c) {
+  switch (ab) {
+#define GQK_CASE(k) case k: return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(a, b, c, 3, k, 0);
+    GQK_AB8_CASES(GQK_CASE)
+#undef GQK_CASE
+  }
+  return c;
+}
+__device__ __forceinline__ v4f mfma1_bcast8(int ab, float a, float b, v4f c) {
+  switch (ab) {
+#define GQK_CASE(k) case k: return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 3, k, 0);
+    GQK_AB8_CASES(GQK_CASE)
+#undef GQK_CASE
+  }
+  return c;
+}
 
 // Which x operands a kernel broadcasts from registers (the MFMA operands, the group sums).  Every
 // kernel broadcasts both but Q6_K's one-record kernel at G = 2, which keeps both in LDS (0.2 us
@@ -885,6 +904,165 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
+// ---- the slab form (M <= 8, shards of at most one 32-row slab per CU): one workgroup per 32-row
+// half (D_SPLIT) of a 64-row tile over the whole k-range, one wave per pair of super-blocks (lanes
+// 0-31: rows of the slab in super-block 2 w, lanes 32-63: the same rows in 2 w + 1).  The waves'
+// sums (two halves per lane row) combine in LDS in a fixed order: no split-K exchange through
+// memory.  The x operands and group sums broadcast from
+// registers within each half of the wave (the two halves multiply different super-blocks).
+// Each wave stages the x of its own two super-blocks (no barrier before the products: a wave
+// decodes as soon as its own loads land), and the combine's barriers wait for LDS only
+// (s_waitcnt lgkmcnt(0); s_barrier).
+static_assert(WaveX<4>::BYTES == GQK_SLAB_SB_BYTES(4) && WaveX<8>::BYTES == GQK_SLAB_SB_BYTES(8) &&
+              GEMV_TAB_BYTES == GQK_GEMV_TAB_BYTES, "slab LDS sizes of the planner");
+template <int G>
+__host__ __device__ constexpr int slab_lds_bytes(int nb, bool tables) {
+  return nb * WaveX<4 * G>::BYTES + (tables ? GEMV_TAB_BYTES : 0);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One lane's record (row r of the tile in super-block record `c`) against its x region wl.
+template <int G, int T>
+__device__ __forceinline__ void slab_record(const Dec<T>& rec, const uint8_t* wl, const Tabs& tb, const Masks& mk,
+                                            v4f (&acc)[G]) {
+  typedef Dec<T> D;
+  constexpr int MPAD = 4 * G, MPS = D::SUB / 4, NSUB = 256 / D::SUB;
+  constexpr bool BIAS = !(T == GQK_IQ4_NL || T == GQK_IQ4_XS || T == GQK_IQ3_S);
+  constexpr bool XG = x_groups_adjacent<T>();
+  constexpr int NXQ = (NSUB + 7) / 8;
+  const int li = threadIdx.x & 3, bl8 = (threadIdx.x >> 2) & 7;   // the lane's block within its half
+  const uint2* xs = (const uint2*)wl;
+  const float* xsm = (const float*)(wl + WaveX<MPAD>::X) + (D::SUB == 16 ? 0 : 16 * MPAD);
+  // operands broadcast within each half: lane 4 b + i holds token 4 g + i's x at slot 8 j + b % 8
+  // and its sum of group 8 k + b % 8
+  float xq[G][NXQ];
+  if constexpr (BIAS)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < NXQ; ++k) xq[g][k] = xsm[(8 * k + bl8) * MPAD + 4 * g + li];
+  uint2 xa[G];
+#pragma unroll
+  for (int s = 0; s < NSUB; ++s) {
+    float scale, bias;
+    rec.scales(s, scale, bias);
+    v4f C[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) C[g] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int m = 0; m < MPS; ++m) {
+      uint32_t b0, b1;
+      rec.pair(s, m, b0, b1, tb, mk);
+      const v4s B = __builtin_bit_cast(v4s, make_uint2(b0, b1));
+      const int slot = s * MPS + m;
+      if (slot % 8 == 0)
+#pragma unroll
+        for (int g = 0; g < G; ++g) xa[g] = xs[x_slot<MPAD, XG>(slot + bl8, 4 * g + li)];
+#pragma unroll
+      for (int g = 0; g < G; ++g) C[g] = mfma4_bcast8(slot % 8, __builtin_bit_cast(v4s, xa[g]), B, C[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if constexpr (BIAS) acc[g] = mfma1_bcast8(s % 8, xq[g][s / 8], -bias, acc[g]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[g][i] = __builtin_fmaf(scale, C[g][i], acc[g][i]);
+    }
+  }
+}
+
+template <int G, int ONLY>
+__global__ __launch_bounds__(64 * GQK_SLAB_MAX_WAVES) void gemv_slab_kernel(
+    const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
+    int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ bias) {
+  constexpr int MPAD = 4 * G, NI = (8 * MPAD + 63) / 64;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[GQK_SLAB_MAX_LDS];   // x of every super-block, IQ tables
+  const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
+  const int type = dsc[D_TYPE];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int nb = dsc[D_NB];
+  uint8_t* lds_tab = lds + nb * WaveX<MPAD>::BYTES;
+  const bool iq = type == GQK_IQ4_NL || type == GQK_IQ4_XS || type == GQK_IQ3_S;
+  Tabs tb{(const uint32_t*)lds_tab, (const uint2*)lds_tab, (const uint4*)(lds_tab + 4096)};
+  if (iq) {
+    build_tables(lds_tab, type);
+    lds_barrier();
+  }
+  const Masks mk = make_masks();
+  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
+  const int64_t tile = dsc[D_TILE0];
+  const int h = dsc[D_SPLIT];                        // the slab: rows 32 h .. 32 h + 31 of the tile
+  const int q = lane >> 5, r = 32 * h + (lane & 31);
+  const int kr = 2 * wave + q;                       // the lane's super-block (nb odd: the last wave's
+  const bool dummy = kr >= nb;                       // upper half has none and drops its sums)
+  const int kl = dummy ? nb - 1 : kr;
+  v4f acc[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
+
+#define RUN(T)                                                                                           \
+  if ((ONLY == 0 || ONLY == T) && type == T) {                                                           \
+    typedef Dec<T> D;                                                                                    \
+    const uint8_t* tb0 = packed + off + tile * nb * (int64_t)(64 * D::REC);                            \
+    uint4 xv0[NI][4], xv1[NI][4];                                                                        \
+    const int s0 = 2 * wave, s1 = min(2 * wave + 1, nb - 1);                                             \
+    stage_load<MPAD>(x, ldx, M, s0, lane, xv0);                                                          \
+    stage_load<MPAD>(x, ldx, M, s1, lane, xv1);                                                          \
+    D rec;                                                                                               \
+    rec.load(tb0 + (int64_t)kl * (64 * D::REC), r);                                                      \
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(lds + s0 * WaveX<MPAD>::BYTES, lane, xv0);        \
+    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(lds + s1 * WaveX<MPAD>::BYTES, lane, xv1);        \
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                                   \
+    slab_record<G, T>(rec, lds + kl * WaveX<MPAD>::BYTES, tb, mk, acc);                                  \
+  }
+  RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
+  RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
+#undef RUN
+  if (dummy)
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // combine: each wave's 64 lanes into its own x region (free once its products are done), one
+  // barrier, then thread o sums output (token o / 32, row o % 32) over the waves in order, each
+  // wave's two halves in order
+  v4f* red = (v4f*)(lds + 2 * wave * WaveX<MPAD>::BYTES);   // [g][lane]
+#pragma unroll
+  for (int g = 0; g < G; ++g) red[g * 64 + lane] = acc[g];
+  lds_barrier();
+  for (int o = threadIdx.x; o < 32 * MPAD; o += blockDim.x) {
+    const int t = o >> 5, rho = o & 31, g = t >> 2, i = t & 3;
+    float sum = 0.f;
+    for (int w = 0; w < nw; ++w) {
+      const float* rw = (const float*)(lds + 2 * w * WaveX<MPAD>::BYTES);
+      sum += rw[(g * 64 + rho) * 4 + i];
+      sum += rw[(g * 64 + 32 + rho) * 4 + i];
+    }
+    const int rr = 32 * h + rho;
+    if (t < M && rr < dsc[D_NVALID]) {
+      const int64_t col = (int64_t)dsc[D_COL0] + rr;
+      const float bv = bias != nullptr ? __builtin_bit_cast(float, (uint32_t)bias[col] << 16) : 0.f;
+      y[t * ldy + col] = __builtin_bit_cast(uint16_t, (__bf16)(sum + bv));
+    }
+  }
+}
+
+template <int G>
+static void launch_slab(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
+                        const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, const uint16_t* bias) {
+  const size_t lds = 0;   // static: GQK_SLAB_MAX_LDS (one workgroup per CU)
+  const dim3 block(64 * nw);
+  switch (only) {
+#define C(T) case T: hipLaunchKernelGGL((gemv_slab_kernel<G, T>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias); return;
+    C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+    C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
+    default:
+      hipLaunchKernelGGL((gemv_slab_kernel<G, 0>), grid, block, lds, st, packed, desc, x, ldx, M, y, ldy, bias);
+  }
+}
+
 template <int G, bool ONE>
 static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t* packed, const int32_t* desc,
                      const uint16_t* x, int64_t ldx, int M, uint16_t* y, int64_t ldy, const uint16_t* bias,
@@ -904,14 +1082,24 @@ static void launch_g(int only, dim3 grid, int nw, hipStream_t st, const uint8_t*
 
 // types_mask: the single type of every row (> 0) or 0 for a mixed launch
 int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                int M, int G, int nw, bool one, void* y, int64_t ldy, const void* bias, float* partials, int* counters,
-                hipStream_t st) {
-  if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
+                int M, int G, int nw, int bm, int nb, void* y, int64_t ldy, const void* bias, float* partials,
+                int* counters, hipStream_t st) {
   dim3 grid(n_desc);
   float* part = partials;
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
+  if (bm == GQK_GEMV_SLAB) {
+    // one wave per pair of super-blocks, the whole x in LDS
+    if (nw != (nb + 1) / 2 || nw > GQK_SLAB_MAX_WAVES || (G != 1 && G != 2) ||
+        (G == 1 ? slab_lds_bytes<1>(nb, true) : slab_lds_bytes<2>(nb, true)) > GQK_SLAB_MAX_LDS)
+      return GQK_ERR_FORM;
+    if (G == 1) launch_slab<1>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb);
+    else launch_slab<2>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb);
+    return GQK_OK;
+  }
+  if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
+  const bool one = bm == 1;
   if (G == 8) return launch_gemv_mid(packed, desc, n_desc, types_mask, x, ldx, M, nw, y, ldy, bias, partials, counters, st);
   switch (G) {
 #define L(GG)                                                                                              \

@@ -244,19 +244,21 @@ def device_workspace(device: torch.device, need: int = 0) -> torch.Tensor:
 
 
 def prepare_grouped_layer(tiles_list: list[torch.Tensor], n_outs: list[int], wtypes: list[int], K: int,
-                          target_wgs: int = 0) -> GroupedLayer:
+                          target_wgs: int = 0, cus: int = 0) -> GroupedLayer:
     """The loader's step for a run of shards already repacked: one packed buffer (the shards'
     tiles back to back; the views replace the separate tensors) and the descriptor tables of
-    every batch-row bucket, uploaded once so the op never builds one at call time."""
+    every batch-row bucket, uploaded once so the op never builds one at call time.  cus: the CU
+    count the plans are made for (0: the current device's; any count gives plans that run
+    correctly on any device)."""
     for t, n, wt in zip(tiles_list, n_outs, wtypes):
         if t.numel() != tiles_bytes(wt, n, K):
             raise ValueError(f"prepare_grouped_layer: tiles of a {n} x {K} shard of type {wt} have {t.numel()} bytes")
     packed = torch.cat([t.reshape(-1) for t in tiles_list]) if len(tiles_list) > 1 else tiles_list[0].reshape(-1)
-    return grouped_layer_from_packed(packed, n_outs, wtypes, K, target_wgs)
+    return grouped_layer_from_packed(packed, n_outs, wtypes, K, target_wgs, cus)
 
 
 def grouped_layer_from_packed(packed: torch.Tensor, n_outs: list[int], wtypes: list[int], K: int,
-                              target_wgs: int = 0) -> GroupedLayer:
+                              target_wgs: int = 0, cus: int = 0) -> GroupedLayer:
     """A grouped layer over a buffer that already holds the shards' tiles back to back (the
     GGUF load path uploads each tensor straight into its slice)."""
     sizes = [tiles_bytes(wt, n, K) for n, wt in zip(n_outs, wtypes)]
@@ -270,7 +272,7 @@ def grouped_layer_from_packed(packed: torch.Tensor, n_outs: list[int], wtypes: l
     gl = GroupedLayer(packed, views, list(n_outs), list(wtypes), K)
     ws = 0
     for m in GEMV_BUCKETS + GEMM_PLAN_M:
-        info, desc = plan(shards, K, m, target_wgs)
+        info, desc = plan(shards, K, m, target_wgs, cus)
         gl.descs.append(desc.to(packed.device))
         gl.plans.extend(info.as_tuple())
         ws = max(ws, info.workspace_bytes)
@@ -278,7 +280,8 @@ def grouped_layer_from_packed(packed: torch.Tensor, n_outs: list[int], wtypes: l
     return gl
 
 
-def pack_layer(raws: list[torch.Tensor], n_outs: list[int], wtypes: list[int], target_wgs: int = 0) -> GroupedLayer:
+def pack_layer(raws: list[torch.Tensor], n_outs: list[int], wtypes: list[int], target_wgs: int = 0,
+               cus: int = 0) -> GroupedLayer:
     """Raw rows of each shard -> repacked, packed and planned (pack_layer,
     gguf-plugin/gluon/tiles_grouped.py:209-212)."""
     Ks = {quant_shape(wt, n, W.shape[1])[1] for W, n, wt in zip(raws, n_outs, wtypes)}
@@ -286,7 +289,7 @@ def pack_layer(raws: list[torch.Tensor], n_outs: list[int], wtypes: list[int], t
         raise ValueError(f"pack_layer: shards have different K {sorted(Ks)}")
     K = Ks.pop()
     return prepare_grouped_layer([repack_tiles(W, n, wt) for W, n, wt in zip(raws, n_outs, wtypes)], n_outs, wtypes, K,
-                                 target_wgs)
+                                 target_wgs, cus)
 
 
 _NPLAN = len(GqkPlanInfo._fields_)

@@ -52,7 +52,9 @@ typedef struct gqk_plan_info {
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
   int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4; 8 = the mid form, 17..32 rows) */
   int32_t bm;         /* GEMM: tokens per tile (64, 128, 256); GEMV (g <= 2): 1 when every wave streams
-                         exactly one 256-weight record (the launch takes the pipeline-free kernel) */
+                         exactly one 256-weight record (the launch takes the pipeline-free kernel),
+                         2 for the slab form (a workgroup per 32-row half tile over the whole k-range,
+                         one wave per pair of super-blocks, no split-K partials) */
   int32_t split;      /* GEMV: most workgroups sharing one tile (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */
@@ -126,7 +128,7 @@ int64_t gqk_linear_workspace_bytes(const gqk_plan_info* info, int M);
 int64_t gqk_workspace_bytes_max(void);
 
 /* Measurement only, no counterpart in the reference: a plain streaming read of `bytes` (a
- * multiple of 1 KiB, at most 2 GiB) at `buf` on `grid` workgroups of `waves` (1..8) waves, each
+ * multiple of 1 KiB, at most 2 GiB) at `buf` on `grid` workgroups of `waves` (1..16) waves, each
  * wave reading one contiguous share and writing one folded word to sink[wave] (grid * waves
  * uint32 words).  Timed over a shard's packed bytes on the shard's own grid it gives the memory
  * floor that bench.py reports beside each launch. */

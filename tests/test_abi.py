@@ -105,6 +105,8 @@ def _check_gemv_rows(shards, K, info, desc):
     nb = K // 256
     d = _rows(desc)
     assert info.form == 1 and d.shape[0] == info.n_desc
+    if info.bm == 2:
+        return _check_slab_rows(shards, K, info, d)
     by_tile = {}
     for row in d:
         assert row[4] == 1 and row[10] == nb
@@ -129,9 +131,62 @@ def _check_gemv_rows(shards, K, info, desc):
     return ncs
 
 
+def _check_slab_rows(shards, K, info, d):
+    """The slab plan's rows: one per 32-row half of each 64-row tile that holds rows (D_SPLIT = the
+    half), each over the whole k-range with no split (D_NC = 1), one wave per pair of super-blocks,
+    no workspace.  Returns {tile: 1}."""
+    nb = K // 256
+    assert info.split == 1 and info.workspace_bytes == 0 and info.nw == (nb + 1) // 2 and info.g <= 2
+    halves = {}
+    col0 = 0
+    cols = {}
+    for wt, n, off in shards:
+        for t in range((n + 63) // 64):
+            cols[(off, t)] = (col0 + 64 * t, min(64, n - 64 * t))
+        col0 += n
+    for row in d:
+        key = (int(row[1]) | int(row[2]) << 32, int(row[3]))
+        assert row[4] == 1 and row[10] == nb and (row[5], row[6]) == (0, nb) and row[12] == 1
+        assert (int(row[8]), int(row[9])) == cols[key]
+        halves.setdefault(key, []).append(int(row[7]))
+    assert set(halves) == set(cols)
+    for key, hs in halves.items():
+        assert hs == ([0, 1] if cols[key][1] > 32 else [0]), key
+    return {k: 1 for k in halves}
+
+
+def test_plan_gemv_slab_form():
+    """The slab form (bm = 2) up to 8 rows: a workgroup per 32-row half tile over the whole
+    k-range when the slabs fill one round of the CUs, at least half of them up to 4 rows and three
+    quarters up to 8, with K <= 6144 (one wave per pair of super-blocks, x of the whole k-range in
+    LDS)."""
+    from gguf_hip import ops
+
+    qkv, o_proj = [(12, 7168, 0)], [(12, 5120, 0)]
+    for M in (1, 4, 5, 8):                                     # qkv: 224 slabs on 256 CUs
+        info, desc = _plan(qkv, 5120, M)
+        assert info.bm == 2 and info.n_desc == 224 and info.nw == 10, M
+        _check_gemv_rows(qkv, 5120, info, desc)
+    for M, bm in ((1, 2), (4, 2), (5, 1), (8, 1)):             # o_proj: 160 slabs, below 3/4 at M > 4
+        assert _plan(o_proj, 5120, M)[0].bm == bm, M
+    assert _plan(qkv, 5120, 9)[0].bm != 2                      # G = 4: not the slab form
+    assert _plan([(12, 9216, 0)], 5120, 1)[0].bm != 2          # 288 slabs: more than one round
+    assert _plan([(12, 2048, 0)], 5120, 1)[0].bm != 2          # 64 slabs: too few CUs busy
+    assert _plan([(12, 7168, 0)], 25 * 256, 8)[0].bm != 2      # 25 super-blocks: above 12 waves
+    info, desc = _plan([(14, 7168, 0)], 24 * 256, 8)           # 24 super-blocks: 12 waves
+    assert info.bm == 2 and info.nw == 12
+    assert _plan(qkv, 5120, 8, 40)[0].bm != 2                  # an explicit wave target keeps split-K
+    # ragged shards and a mixed layer on a pinned CU count: a last tile of <= 32 rows has one slab
+    off = ops.tiles_bytes(12, 200, 5 * 256)
+    mixed = [(12, 200, 0), (23, 232, off)]                    # 7 + 8 slabs, 5 super-blocks (odd)
+    info, desc = _plan(mixed, 5 * 256, 8, cus=16)
+    assert info.bm == 2 and info.n_desc == 15 and info.types_mask == 0 and info.nw == 3
+    _check_gemv_rows(mixed, 5 * 256, info, desc)
+
+
 def test_read_floor_argument_checks():
     """The measurement-only plain read refuses null buffers, sizes that are not whole KiB (or
-    beyond 2 GiB) and grids outside 1..8 waves before any launch."""
+    beyond 2 GiB) and grids outside 1..16 waves before any launch."""
     from gguf_hip import _lib
 
     f = _lib.lib.gqk_read_floor
@@ -140,14 +195,15 @@ def test_read_floor_argument_checks():
     assert f(p, 1000, 1, 1, p, None) == _lib.GQK_ERR_SHAPE
     assert f(p, (1 << 31) + 1024, 1, 1, p, None) == _lib.GQK_ERR_SHAPE
     assert f(p, 1024, 0, 1, p, None) == _lib.GQK_ERR_SHAPE
-    assert f(p, 1024, 1, 9, p, None) == _lib.GQK_ERR_SHAPE
+    assert f(p, 1024, 1, 17, p, None) == _lib.GQK_ERR_SHAPE
     assert "read_floor" in _lib.lib.gqk_last_error().decode()
 
 
 def test_plan_gemv_balanced_split_partition():
     from gguf_hip import _lib, ops
 
-    for target in (1, 16, 97, 1024, 4096, 0):
+    assert _plan([(21, 6144, 0)], 20 * 256, 1, 0)[0].bm == 2   # the default plan: 192 slabs (slab form)
+    for target in (1, 16, 97, 1024, 4096):
         info, desc = _plan([(21, 6144, 0)], 20 * 256, 1, target)
         ncs = _check_gemv_rows([(21, 6144, 0)], 20 * 256, info, desc)
         S, nw = info.split, info.nw
@@ -161,8 +217,8 @@ def test_plan_gemv_balanced_split_partition():
     assert _plan([(21, 6144, 0)], 20 * 256, 1, 1)[0].nw == 1
     info = _plan([(21, 6144, 0)], 20 * 256, 1, 4096)[0]
     assert (info.nw, info.split) == (4, 5)                  # 43 waves per tile wanted: 4 x min(11, 20 // 4)
-    info = _plan([(21, 6144, 0)], 20 * 256, 8, 0)[0]
-    assert (info.nw, info.split) == (4, 5)                  # default target 2048 waves: 22 per tile
+    info = _plan([(21, 6144, 0)], 20 * 256, 8, 2048)[0]
+    assert (info.nw, info.split) == (4, 5)                  # the default wave target, 2048: 22 per tile
 
 
 def test_plan_gemv_tail_tiles_split():
@@ -205,17 +261,17 @@ def test_plan_gemv_tail_tiles_split():
         assert info.bm == bm and info.types_mask == 0, M
         if bm:
             assert set(_check_gemv_rows(mixed, 5120, info, desc).values()) == {5} and info.n_desc == 192 * 5
-    assert _plan([(12, 7168, 0)], 5120, 8, 0)[0].bm == 1 and _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
+    assert _plan([(12, 5120, 0)], 5120, 8, 0)[0].bm == 1 and _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
     # one round of split tiles with >= 2 records a wave fills the 512 slots exactly: down 5120 x
-    # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; qkv (1 record a wave) keeps 5 each
+    # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; o_proj (1 record a wave) keeps 5 each
     info, desc = _plan([(12, 5120, 0)], 17408, 8, 0)
     ncs = _check_gemv_rows([(12, 5120, 0)], 17408, info, desc)
     assert info.n_desc == 512 and sorted(ncs.values()) == [6] * 48 + [7] * 32 and info.split == 7
-    info, desc = _plan([(12, 7168, 0)], 5120, 8, 0)
-    assert set(_check_gemv_rows([(12, 7168, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 560
-    # the GEMV's bm field flags plans whose waves all stream exactly one record (qkv, o_proj at
-    # K = 5120: 20 records = 5 workgroups x 4 waves); the pipeline-free kernel serves them
-    assert info.bm == 1 and _plan([(12, 5120, 0)], 5120, 1, 0)[0].bm == 1
+    info, desc = _plan([(12, 5120, 0)], 5120, 8, 0)
+    assert set(_check_gemv_rows([(12, 5120, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 400
+    # the GEMV's bm field flags plans whose waves all stream exactly one record (o_proj at K = 5120:
+    # 20 records = 5 workgroups x 4 waves); the pipeline-free kernel serves them
+    assert info.bm == 1 and _plan([(12, 9216, 0)], 5120, 1, 0)[0].bm == 1
     assert _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0 and _plan([(12, 5120, 0)], 17408, 8, 0)[0].bm == 0
     # small targets: 10 tiles on 8 slots of 2 waves... (target 16) -> the last 2 tiles split
     info, desc = _plan([(12, 64 * 9 + 17, 0)], 16 * 256, 1, 16)
@@ -230,7 +286,7 @@ def test_plan_all_split_rows_interleaved_by_xcd():
     a plan with whole tiles keeps the tile order."""
     from gguf_hip import ops
 
-    for shards, K, M in (([(12, 5120, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 7168, 0)], 5120, 1),
+    for shards, K, M in (([(12, 5120, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 9216, 0)], 5120, 1),
                          ([(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))], 5120, 8)):
         info, desc = _plan(shards, K, M)
         d = _rows(desc)

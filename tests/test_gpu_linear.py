@@ -384,6 +384,65 @@ def test_linear_method_unquantized_shard_splits_runs(dev):
     assert bool((big[:, :20] == 7).all()) and bool((big[:, 84:] == 7).all())
 
 
+def _plan_of(gl, M):
+    from gguf_hip import ops
+
+    return ops.GqkPlanInfo.from_tuple(gl.plans[ops._pick_plan(gl.plans, M) * ops._NPLAN:][:ops._NPLAN])
+
+
+@pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
+def test_gemv_slab_form(dev, wt):
+    """The slab form (up to 8 rows: a workgroup per 32-row half tile over the whole k-range, each
+    wave's x in LDS, the waves combined in LDS in a fixed order), planned on a pinned CU count so
+    that small shards take it: a last tile of <= 32 and of > 32 rows, an odd super-block count (a
+    half wave without a super-block), the largest k-range (24 super-blocks, 12 waves), a fused
+    bias, bit-identical repeats; against the oracle."""
+    import gguf_hip
+
+    rng = np.random.default_rng(900 + wt)
+    for n, nbk, cus in ((200, 5, 8), (232, 4, 8), (100, 24, 4)):
+        K = nbk * 256
+        raw = G.random_blocks(rng, n, K, wt)
+        wf = G.dequantize(raw, wt)
+        gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt], cus=cus)
+        bias = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 4).to(torch.bfloat16).to(dev)
+        for M in (1, 3, 4, 5, 8):
+            assert _plan_of(gl, M).bm == 2, (n, nbk, M)
+            x = _x(M, K, 3000 + M, dev)
+            y = gguf_hip.mul_mat_grouped(x, gl, bias)
+            e = G.rel_err(y.float().cpu().numpy(), _ref(x, wf) + bias.float().cpu().numpy()[None])
+            assert e < TOL, (G.NAMES[wt], n, nbk, M, e)
+            assert torch.equal(y, gguf_hip.mul_mat_grouped(x, gl, bias)), "not deterministic"
+        # the same layer planned for the device: same results within the tolerance
+        gd = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt])
+        x = _x(8, K, 3100, dev)
+        assert G.rel_err(gguf_hip.mul_mat_grouped(x, gd).float().cpu().numpy(), _ref(x, wf)) < TOL
+
+
+def test_gemv_slab_form_mixed_layer(dev):
+    """A mixed-type layer (Q4_K, IQ4_XS with its LDS tables, Q6_K) in the slab form, written into a
+    column slice of a wider output."""
+    import gguf_hip
+
+    rng = np.random.default_rng(77)
+    K = 5 * 256
+    shards = [(G.Q4_K, 200), (G.IQ4_XS, 232), (G.Q6_K, 96)]
+    raws = [G.random_blocks(rng, n, K, wt) for wt, n in shards]
+    wf = np.concatenate([G.dequantize(r, wt) for r, (wt, _) in zip(raws, shards)])
+    gl = gguf_hip.pack_layer([torch.from_numpy(r).to(dev) for r in raws], [n for _, n in shards],
+                             [wt for wt, _ in shards], cus=20)
+    n_total = sum(n for _, n in shards)
+    for M in (2, 8):
+        info = _plan_of(gl, M)
+        assert info.bm == 2 and info.types_mask == 0, M
+        x = _x(M, K, 4000 + M, dev)
+        out = torch.full((M, n_total + 40), 7.0, dtype=torch.bfloat16, device=dev)
+        gguf_hip.mul_mat_grouped(x, gl, out=out[:, 20:20 + n_total])
+        o = out.float().cpu().numpy()
+        assert (o[:, :20] == 7).all() and (o[:, 20 + n_total:] == 7).all()
+        assert G.rel_err(o[:, 20:20 + n_total], _ref(x, wf)) < TOL, M
+
+
 def test_fused_bias(dev):
     """A bf16 bias is added in the kernels' epilogue (direct GEMV store, split-K fixup, GEMM and
     stream-K fixup): a zero bias changes no bit, a random one matches oracle + bias; an fp32 bias
