@@ -904,6 +904,30 @@ void gemv_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
+// x of super-block kb through whole 128-byte lines (MPAD = 8): load j (0..3) of lane l reads
+// token t = l / 8's 16-byte piece u = 8 j + ((l % 8) ^ ((t >> 1) & 3)), so each load covers 8
+// full lines (the item order of stage_load touches 32 lines per load, 32 bytes of each).  The
+// pieces go to LDS in lane order (region + 1 KiB j + 16 l), come back in stage_load's item order
+// (lane it: token it % 8, 32 weights it / 8; the swizzle puts every quarter-wave's 16 reads in
+// distinct banks) and then take the usual stage_store, all within the super-block's own x
+// region (the raw pieces are read before any slot is written: a wave's LDS accesses run in
+// order).
+__device__ __forceinline__ void stage_load_lines(const uint16_t* __restrict__ x, int64_t ldx, int M, int kb, int lane,
+                                                 uint4 (&v)[4]) {
+  const int t = lane >> 3, c = (lane & 7) ^ ((t >> 1) & 3);
+  const uint16_t* p = x + (int64_t)min(t, M - 1) * ldx + (int64_t)kb * 256 + 8 * c;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = *(const uint4*)(p + 64 * j);
+}
+__device__ __forceinline__ void stage_lines_to_items(uint8_t* wl, int lane, const uint4 (&v)[4], uint4 (&o)[1][4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *(uint4*)(wl + 1024 * j + 16 * lane) = v[j];
+  const int t = lane & 7, s32 = lane >> 3, f = (t >> 1) & 3;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    o[0][q] = *(const uint4*)(wl + 1024 * (s32 >> 1) + 16 * (8 * t + ((4 * (s32 & 1) + q) ^ f)));
+}
+
 // ---- the slab form (M <= 8, shards of at most one 32-row slab per CU): one workgroup per 32-row
 // half (D_SPLIT) of a 64-row tile over the whole k-range, one wave per pair of super-blocks (lanes
 // 0-31: rows of the slab in super-block 2 w, lanes 32-63: the same rows in 2 w + 1).  The waves'
@@ -1008,12 +1032,27 @@ __global__ __launch_bounds__(64 * GQK_SLAB_MAX_WAVES) void gemv_slab_kernel(
     const uint8_t* tb0 = packed + off + tile * nb * (int64_t)(64 * D::REC);                            \
     uint4 xv0[NI][4], xv1[NI][4];                                                                        \
     const int s0 = 2 * wave, s1 = min(2 * wave + 1, nb - 1);                                             \
-    stage_load<MPAD>(x, ldx, M, s0, lane, xv0);                                                          \
-    stage_load<MPAD>(x, ldx, M, s1, lane, xv1);                                                          \
+    uint8_t* w0 = lds + s0 * WaveX<MPAD>::BYTES;                                                         \
+    uint8_t* w1 = lds + s1 * WaveX<MPAD>::BYTES;                                                         \
     D rec;                                                                                               \
-    rec.load(tb0 + (int64_t)kl * (64 * D::REC), r);                                                      \
-    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(lds + s0 * WaveX<MPAD>::BYTES, lane, xv0);        \
-    stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(lds + s1 * WaveX<MPAD>::BYTES, lane, xv1);        \
+    if constexpr (MPAD == 8) {                                                                           \
+      uint4 l0[4], l1[4];                                                                                \
+      stage_load_lines(x, ldx, M, s0, lane, l0);                                                         \
+      stage_load_lines(x, ldx, M, s1, lane, l1);                                                         \
+      rec.load(tb0 + (int64_t)kl * (64 * D::REC), r);                                                    \
+      stage_lines_to_items(w0, lane, l0, xv0);                                                           \
+      stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(w0, lane, xv0);                                  \
+      if (s1 != s0) {                                                                                    \
+        stage_lines_to_items(w1, lane, l1, xv1);                                                         \
+        stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(w1, lane, xv1);                                \
+      }                                                                                                  \
+    } else {                                                                                             \
+      stage_load<MPAD>(x, ldx, M, s0, lane, xv0);                                                        \
+      stage_load<MPAD>(x, ldx, M, s1, lane, xv1);                                                        \
+      rec.load(tb0 + (int64_t)kl * (64 * D::REC), r);                                                    \
+      stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(w0, lane, xv0);                                  \
+      stage_store<MPAD, D::FAM, x_groups_adjacent<T>()>(w1, lane, xv1);                                  \
+    }                                                                                                    \
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");                                                   \
     slab_record<G, T>(rec, lds + kl * WaveX<MPAD>::BYTES, tb, mk, acc);                                  \
   }
