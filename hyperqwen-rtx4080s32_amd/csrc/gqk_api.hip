@@ -286,10 +286,10 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // The slab form (up to 8 rows): a workgroup per 32-row half of a tile over the whole k-range,
     // one wave per pair of super-blocks, each staging its own x in LDS; no split-K exchange.  One
     // workgroup per CU, so its time follows the slab's bytes, not the shard's: taken when the
-    // slabs fill one round of the CUs, at least half of them up to 4 rows and three quarters up
-    // to 8.  Measured on 256 CUs against the split-K plans (eight types, µs): qkv 7168 x 5120
-    // (224 slabs) 0.3-1.7 faster at M = 1 / 4 and 0.2-1.5 at M = 8; o_proj 5120 x 5120 (160 slabs)
-    // 0.3-0.6 faster at M = 1 / 4, but at M = 8 even to 0.7 slower (Q4_K 9.1 -> 9.8).
+    // slabs fill one round of the CUs, at least half of them.  Measured on 256 CUs against the
+    // split-K plans (eight types, µs): qkv 7168 x 5120 (224 slabs) 0.3-1.7 faster at M = 1 / 4 and
+    // 0.2-1.8 at M = 8; o_proj 5120 x 5120 (160 slabs) 0.3-0.6 faster at M = 1 / 4, and at M = 6 / 8
+    // 0.1-0.7 faster for Q5_K, IQ4_XS, Q8_0, Q4_0, Q2_K, even for Q4_K, Q6_K, IQ3_S.
     int64_t slabs = 0;
     bool any_iq = false;
     for (int i = 0; i < nshards; ++i) {
@@ -300,7 +300,7 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     }
     const bool slab = target_wgs <= 0 && pi.g <= 2 && nb <= 2 * GQK_SLAB_MAX_WAVES &&
                       nb * GQK_SLAB_SB_BYTES(pi.m_max) + (any_iq ? GQK_GEMV_TAB_BYTES : 0) <= GQK_SLAB_MAX_LDS &&
-                      (pi.g == 1 ? 2 * slabs >= cus : 4 * slabs >= 3 * (int64_t)cus) && slabs <= cus;
+                      2 * slabs >= cus && slabs <= cus;
     if (slab) {
       pi.bm = GQK_GEMV_SLAB;
       pi.nw = (int32_t)((nb + 1) / 2);

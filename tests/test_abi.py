@@ -157,9 +157,8 @@ def _check_slab_rows(shards, K, info, d):
 
 def test_plan_gemv_slab_form():
     """The slab form (bm = 2) up to 8 rows: a workgroup per 32-row half tile over the whole
-    k-range when the slabs fill one round of the CUs, at least half of them up to 4 rows and three
-    quarters up to 8, with K <= 6144 (one wave per pair of super-blocks, x of the whole k-range in
-    LDS)."""
+    k-range when the slabs fill one round of the CUs, at least half of them, with K <= 6144 (one
+    wave per pair of super-blocks, each staging its own x in LDS)."""
     from gguf_hip import ops
 
     qkv, o_proj = [(12, 7168, 0)], [(12, 5120, 0)]
@@ -167,8 +166,9 @@ def test_plan_gemv_slab_form():
         info, desc = _plan(qkv, 5120, M)
         assert info.bm == 2 and info.n_desc == 224 and info.nw == 10, M
         _check_gemv_rows(qkv, 5120, info, desc)
-    for M, bm in ((1, 2), (4, 2), (5, 1), (8, 1)):             # o_proj: 160 slabs, below 3/4 at M > 4
-        assert _plan(o_proj, 5120, M)[0].bm == bm, M
+    for M in (1, 4, 5, 8):                                     # o_proj: 160 slabs
+        assert _plan(o_proj, 5120, M)[0].bm == 2, M
+    assert _plan([(12, 3968, 0)], 5120, 8)[0].bm != 2          # 124 slabs: under half the CUs
     assert _plan(qkv, 5120, 9)[0].bm != 2                      # G = 4: not the slab form
     assert _plan([(12, 9216, 0)], 5120, 1)[0].bm != 2          # 288 slabs: more than one round
     assert _plan([(12, 2048, 0)], 5120, 1)[0].bm != 2          # 64 slabs: too few CUs busy
@@ -261,15 +261,15 @@ def test_plan_gemv_tail_tiles_split():
         assert info.bm == bm and info.types_mask == 0, M
         if bm:
             assert set(_check_gemv_rows(mixed, 5120, info, desc).values()) == {5} and info.n_desc == 192 * 5
-    assert _plan([(12, 5120, 0)], 5120, 8, 0)[0].bm == 1 and _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
+    assert _plan([(12, 3072, 0)], 5120, 8, 0)[0].bm == 1 and _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0
     # one round of split tiles with >= 2 records a wave fills the 512 slots exactly: down 5120 x
     # 17408 (80 tiles, 68 records) as 32 tiles x 7 + 48 x 6; o_proj (1 record a wave) keeps 5 each
     info, desc = _plan([(12, 5120, 0)], 17408, 8, 0)
     ncs = _check_gemv_rows([(12, 5120, 0)], 17408, info, desc)
     assert info.n_desc == 512 and sorted(ncs.values()) == [6] * 48 + [7] * 32 and info.split == 7
-    info, desc = _plan([(12, 5120, 0)], 5120, 8, 0)
-    assert set(_check_gemv_rows([(12, 5120, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 400
-    # the GEMV's bm field flags plans whose waves all stream exactly one record (o_proj at K = 5120:
+    info, desc = _plan([(12, 3072, 0)], 5120, 8, 0)
+    assert set(_check_gemv_rows([(12, 3072, 0)], 5120, info, desc).values()) == {5} and info.n_desc == 240
+    # the GEMV's bm field flags plans whose waves all stream exactly one record (3072 x 5120:
     # 20 records = 5 workgroups x 4 waves); the pipeline-free kernel serves them
     assert info.bm == 1 and _plan([(12, 9216, 0)], 5120, 1, 0)[0].bm == 1
     assert _plan([(12, 34816, 0)], 5120, 8, 0)[0].bm == 0 and _plan([(12, 5120, 0)], 17408, 8, 0)[0].bm == 0
@@ -286,7 +286,7 @@ def test_plan_all_split_rows_interleaved_by_xcd():
     a plan with whole tiles keeps the tile order."""
     from gguf_hip import ops
 
-    for shards, K, M in (([(12, 5120, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 9216, 0)], 5120, 1),
+    for shards, K, M in (([(12, 3072, 0)], 5120, 8), ([(14, 5120, 0)], 17408, 8), ([(12, 9216, 0)], 5120, 1),
                          ([(12, 7168, 0), (14, 5120, ops.tiles_bytes(12, 7168, 5120))], 5120, 8)):
         info, desc = _plan(shards, K, M)
         d = _rows(desc)
