@@ -29,7 +29,9 @@ extern "C" {
 #define GQK_ERR_ARG (-5)   /* null pointer or bad argument */
 
 #define GQK_FORM_GEMV 1 /* M <= 32, every type: streaming forms over (tile, k-range) rows: the in-register
-                           decode GEMV up to 16 rows, the mid form (g = 8) for 17..32 */
+                           decode GEMV up to 16 rows (small shards up to 8 rows in its slab form,
+                           plan bm = 2: a row per 32-row slab over the whole k-range), the mid form
+                           (g = 8) for 17..32 */
 #define GQK_FORM_GEMM 2 /* M > 32: LDS-dequant bf16 MFMA GEMM (any M) */
 
 #define GQK_CTR_BYTES 262144 /* the arrival-counter region at the start of every workspace */
