@@ -1,7 +1,8 @@
 """gqk_linear_noalloc (the entry point that allocates nothing: its workspace is a per-GPU device
 array) against gqk_linear with a caller workspace, through the C ABI: bit-identical outputs on
-two calls in a row, the second with fewer rows, for a split-K GEMV plan, a stream-K GEMM plan and
-a mixed-type layer; a plan whose workspace exceeds the array is refused with an error."""
+two calls in a row, the second with fewer rows, for a split-K GEMV plan, a slab-form GEMV plan (no
+workspace at all), a stream-K GEMM plan and a mixed-type layer; a plan whose workspace exceeds the
+array is refused with an error."""
 import ctypes
 
 import numpy as np
@@ -44,15 +45,16 @@ def test_noalloc_matches_linear_twice_then_smaller(dev):
     rng = np.random.default_rng(41)
     K = 3072
     cases = [
-        ("split-K GEMV", [(G.Q4_K, 900)], 4096, (8, 3)),
-        ("stream-K GEMM", [(G.Q6_K, 1000)], 0, (60, 20)),
-        ("mixed layer", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 2048, (5, 2)),
-        ("mixed layer GEMM", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 0, (100, 33)),
+        ("split-K GEMV", [(G.Q4_K, 900)], 4096, 0, (8, 3)),
+        ("slab GEMV", [(G.Q6_K, 200)], 0, 8, (8, 3)),             # planned for 8 CUs: 7 slabs
+        ("stream-K GEMM", [(G.Q6_K, 1000)], 0, 0, (60, 20)),
+        ("mixed layer", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 2048, 0, (5, 2)),
+        ("mixed layer GEMM", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 0, 0, (100, 33)),
     ]
-    for name, shards, target, Ms in cases:
+    for name, shards, target, cus, Ms in cases:
         raws = [G.random_blocks(rng, n, K, wt) for wt, n in shards]
         gl = gguf_hip.pack_layer([torch.from_numpy(r).to(dev) for r in raws], [n for _, n in shards],
-                                 [wt for wt, _ in shards], target_wgs=target)
+                                 [wt for wt, _ in shards], target_wgs=target, cus=cus)
         for M in Ms:                                          # two calls in a row, the second smaller
             x = _x(M, K, 17 + M, dev)
             rc, y_ref, info = _call(None, gl, x, True)
@@ -65,6 +67,8 @@ def test_noalloc_matches_linear_twice_then_smaller(dev):
             assert G.rel_err(y.float().cpu().numpy(), G.matmul_ref(x.float().cpu().numpy(), wf)) < 1e-2, (name, M)
         if name == "split-K GEMV":
             assert info.split > 1
+        if name == "slab GEMV":
+            assert info.bm == 2 and info.workspace_bytes == 0
 
 
 def test_noalloc_refuses_a_plan_beyond_its_array(dev):
