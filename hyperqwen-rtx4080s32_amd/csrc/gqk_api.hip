@@ -290,18 +290,32 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // split-K plans (eight types, µs): qkv 7168 x 5120 (224 slabs) 0.3-1.7 faster at M = 1 / 4 and
     // 0.2-1.8 at M = 8; o_proj 5120 x 5120 (160 slabs) 0.3-0.6 faster at M = 1 / 4, and at M = 6 / 8
     // 0.1-0.7 faster for Q5_K, IQ4_XS, Q8_0, Q4_0, Q2_K, even for Q4_K, Q6_K, IQ3_S.
+    //
+    // From 17 rows the mid form's slab (32 x 32 MFMA blocks, x staged per step) replaces the mid
+    // form's split-K exchange, whose 8 KiB of partials per workgroup cost ~30% of its launches
+    // (eleven types at M = 17 / 32: qkv 5.6-9.8 us faster, o_proj 3.0-5.1; Q4_K qkv 20.7 -> 13.4 us
+    // at 32).  At 9..16 rows it also beats the G = 4 GEMV when the slabs nearly fill the CUs (qkv,
+    // 224 of 256: 1.0-3.5 us faster at 12, except IQ3_S, 0.6-0.8 slower); at 160 slabs (o_proj) half the types are
+    // slower there, and up to 8 rows the GEMV slab is 1.5-4.8 us faster than it.  `down` (68
+    // super-blocks, 12 waves of ~6) measured 3-7 us slower than split-K at 24-32 rows.
     int64_t slabs = 0;
-    bool any_iq = false;
+    bool any_iq = false, any_iq3s = false;
     for (int i = 0; i < nshards; ++i) {
       const int64_t rem = shards[i].n % 64;
       slabs += 2 * ((shards[i].n + 63) / 64) - (rem != 0 && rem <= 32 ? 1 : 0);
       const int t = shards[i].ggml_type;
       any_iq |= t == GQK_IQ4_NL || t == GQK_IQ4_XS || t == GQK_IQ3_S;
+      any_iq3s |= t == GQK_IQ3_S;
     }
-    const bool slab = target_wgs <= 0 && pi.g <= 2 && nb <= 2 * GQK_SLAB_MAX_WAVES &&
-                      nb * GQK_SLAB_SB_BYTES(pi.m_max) + (any_iq ? GQK_GEMV_TAB_BYTES : 0) <= GQK_SLAB_MAX_LDS &&
-                      2 * slabs >= cus && slabs <= cus;
+    const bool slab_fit =
+        pi.g <= 2 ? nb * GQK_SLAB_SB_BYTES(pi.m_max) + (any_iq ? GQK_GEMV_TAB_BYTES : 0) <= GQK_SLAB_MAX_LDS
+                  : pi.g == 8 || (8 * slabs >= 7 * cus && !any_iq3s);
+    const bool slab = target_wgs <= 0 && nb <= 2 * GQK_SLAB_MAX_WAVES && slab_fit && 2 * slabs >= cus && slabs <= cus;
     if (slab) {
+      if (pi.g == 4) {   // served by the mid form's slab (x padded to 32 tokens)
+        pi.g = 8;
+        pi.m_max = 32;
+      }
       pi.bm = GQK_GEMV_SLAB;
       pi.nw = (int32_t)((nb + 1) / 2);
       pi.split = 1;

@@ -853,10 +853,10 @@ __global__ __launch_bounds__(GE::NT) __attribute__((amdgpu_waves_per_eu(GE::WPE)
 // IQ4_XS gate_up 0.94; Q6_K and Q8_0 gate_up 1.04).  Tried: weights two steps ahead (more
 // registers, fewer waves: 0-8% slower) and 64 tokens per wave (226-260 VGPRs: 23-45% slower than
 // the 64 x 128 GEMM form, which keeps 33..64 rows).
-template <int T>
+template <int T, int NRB = 2>
 __device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, const uint16_t* __restrict__ x, int64_t ldx,
                                          int M, uint16_t* xl, int kw0, int kw1, int c, int r, const GTabs& tb,
-                                         v16f (&acc)[2]) {
+                                         v16f (&acc)[NRB], int r0 = 0) {
   constexpr int REC = gqk_layout<T>::REC;
   if (kw0 >= kw1) return;
   // k offsets (within a 64-weight step) of the lane's four 8-weight chunks, in MFMA order
@@ -875,14 +875,14 @@ __device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, cons
     xsrc[i] = x + (int64_t)min(t, M - 1) * ldx + 8 * ((lane & 7) ^ ((t >> 1) & 7));
   }
   const int rs = (r >> 1) & 7;
-  struct Step { B2<T> w[2]; v4u xg[4]; };
+  struct Step { B2<T> w[NRB]; v4u xg[4]; };
   Step p0, p1;
   auto load = [&](Step& p, int s) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) p.xg[i] = *(const v4u*)(xsrc[i] + (int64_t)s * 64);
     const uint8_t* rc = tbase + (int64_t)(s >> 2) * (64 * REC);
-    p.w[0].load(rc, r, s & 3, c);
-    p.w[1].load(rc, 32 + r, s & 3, c);
+#pragma unroll
+    for (int b = 0; b < NRB; ++b) p.w[b].load(rc, r0 + 32 * b + r, s & 3, c);
   };
   auto compute = [&](const Step& p, int s) __attribute__((always_inline)) {
 #pragma unroll
@@ -891,7 +891,7 @@ __device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, cons
 #pragma unroll
     for (int q = 0; q < 4; ++q) a[q] = *(const v8bf*)(xl + (r * 8 + ((koff[q] >> 3) ^ rs)) * 8);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NRB; ++b) {
       const GS st = p.w[b].prep(s & 3, c);
       uint32_t o[16];
 #pragma unroll
@@ -1042,13 +1042,99 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
+// The mid form's slab variant (17..32 rows, shards of at most one 32-row slab per CU): one
+// workgroup per 32-row half (D_SPLIT) of a 64-row tile over the whole k-range, its waves splitting
+// the k-range as in the mid form (two super-blocks each at K = 5120) with one 32 x 32 block of
+// rows each; no split-K partials (whose 8 KiB per workgroup at 32 tokens made the exchange ~30% of
+// the mid form's qkv / o_proj launches).  Each wave's sums go to its own 4 KiB x region once its
+// products are done, and after one barrier every thread sums one output over the waves in order.
+template <int ONLY>
+__global__ __launch_bounds__(64 * GQK_SLAB_MAX_WAVES) void gemv_mid_slab_kernel(
+    const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc, const uint16_t* __restrict__ x,
+    int64_t ldx, int M, uint16_t* __restrict__ y, int64_t ldy, const uint16_t* __restrict__ bias) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[GB_TAB_BYTES];
+  __shared__ __attribute__((aligned(16))) uint16_t xlds[GQK_SLAB_MAX_WAVES * 2048];   // a 4 KiB x step per wave
+  const int32_t* dsc = desc + (int64_t)blockIdx.x * GQK_DESC_WORDS;
+  const int type = dsc[D_TYPE];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+  const int c = lane >> 5, r = lane & 31;
+  GTabs tb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    tb.kv[i] = (uint32_t)(c_kvalues[4 * i] + 128) | ((uint32_t)(c_kvalues[4 * i + 1] + 128) << 8) |
+               ((uint32_t)(c_kvalues[4 * i + 2] + 128) << 16) | ((uint32_t)(c_kvalues[4 * i + 3] + 128) << 24);
+  tb.grid = (uint32_t*)lds;
+  tb.sign = (uint4*)(lds + 512 * 4);
+  if ((ONLY == 0 || ONLY == GQK_IQ3_S) && type == GQK_IQ3_S) {   // uniform over the workgroup
+    uint32_t* grid = (uint32_t*)lds;
+    uint4* sign = (uint4*)(lds + 512 * 4);
+    for (int t = threadIdx.x; t < 512; t += blockDim.x) grid[t] = c_iq3s_grid[t];
+    for (int t = threadIdx.x; t < 256; t += blockDim.x) {
+      uint32_t m[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m[q] = (((t >> (2 * q)) & 1) << 15) | (((t >> (2 * q + 1)) & 1) << 31);
+      sign[t] = make_uint4(m[0], m[1], m[2], m[3]);
+    }
+    __syncthreads();
+  }
+  const int64_t off = (int64_t)(uint32_t)dsc[D_OFF_LO] | ((int64_t)dsc[D_OFF_HI] << 32);
+  const int64_t tile = dsc[D_TILE0];
+  const int h = dsc[D_SPLIT];                        // the slab: rows 32 h .. 32 h + 31 of the tile
+  const int nb = dsc[D_NB], kb0 = dsc[D_KB0], nk = dsc[D_KB1] - kb0;
+  const int kw0 = kb0 + (wave * nk) / nw, kw1 = kb0 + ((wave + 1) * nk) / nw;
+  uint16_t* xl = xlds + wave * 2048;
+  v16f acc[1];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[0][v] = 0.f;
+#define RUN(T)                                                                                                 \
+  if ((ONLY == 0 || ONLY == T) && type == T)                                                                   \
+    mid_wave<T, 1>(packed + off + tile * nb * (int64_t)(64 * gqk_layout<T>::REC), x, ldx, M, xl, kw0, kw1, c, r, tb, \
+                   acc, 32 * h);
+  RUN(GQK_Q4_0) RUN(GQK_Q5_0) RUN(GQK_Q8_0) RUN(GQK_Q2_K) RUN(GQK_Q3_K) RUN(GQK_Q4_K) RUN(GQK_Q5_K) RUN(GQK_Q6_K)
+  RUN(GQK_IQ4_NL) RUN(GQK_IQ3_S) RUN(GQK_IQ4_XS)
+#undef RUN
+
+  // combine: C block lane -> row 32 h + r, tokens 8 (v / 4) + 4 c + v % 4; [v][lane] per wave
+  float* red = (float*)xl;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) red[v * 64 + lane] = acc[0][v];
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  const int nvalid = dsc[D_NVALID];
+  const int64_t col0 = dsc[D_COL0];
+  for (int o = threadIdx.x; o < 32 * 32; o += blockDim.x) {
+    const int t = o >> 5, rho = o & 31;
+    const int v = 4 * (t >> 3) + (t & 3), l = 32 * ((t >> 2) & 1) + rho;
+    float sum = 0.f;
+    for (int w = 0; w < nw; ++w) sum += ((const float*)(xlds + w * 2048))[v * 64 + l];
+    const int row = 32 * h + rho;
+    if (t < M && row < nvalid) {
+      const float bv = bias != nullptr ? __builtin_bit_cast(float, (uint32_t)bias[col0 + row] << 16) : 0.f;
+      y[(int64_t)t * ldy + col0 + row] = __builtin_bit_cast(uint16_t, (__bf16)(sum + bv));
+    }
+  }
+}
+
 int launch_gemv_mid(const uint8_t* packed, const int32_t* desc, int n_desc, int types_mask, const void* x, int64_t ldx,
-                    int M, int nw, void* y, int64_t ldy, const void* bias, float* part, int* ctr, hipStream_t st) {
-  if (nw < 1 || nw > 4) return GQK_ERR_FORM;
-  const dim3 grid(n_desc), block(64 * nw);
+                    int M, int nw, bool slab, void* y, int64_t ldy, const void* bias, float* part, int* ctr,
+                    hipStream_t st) {
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
+  if (slab) {
+    if (nw < 1 || nw > GQK_SLAB_MAX_WAVES) return GQK_ERR_FORM;
+    const dim3 grid(n_desc), block(64 * nw);
+    switch (types_mask) {
+#define C(T) case T: hipLaunchKernelGGL((gemv_mid_slab_kernel<T>), grid, block, 0, st, packed, desc, xx, ldx, M, yy, ldy, bb); return GQK_OK;
+      C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)
+      C(GQK_IQ4_NL) C(GQK_IQ3_S) C(GQK_IQ4_XS)
+#undef C
+      default:
+        hipLaunchKernelGGL((gemv_mid_slab_kernel<0>), grid, block, 0, st, packed, desc, xx, ldx, M, yy, ldy, bb);
+    }
+    return GQK_OK;
+  }
+  if (nw < 1 || nw > 4) return GQK_ERR_FORM;
+  const dim3 grid(n_desc), block(64 * nw);
   switch (types_mask) {
 #define C(T) case T: hipLaunchKernelGGL((gemv_mid_kernel<T>), grid, block, 0, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, ctr); return GQK_OK;
     C(GQK_Q4_0) C(GQK_Q5_0) C(GQK_Q8_0) C(GQK_Q2_K) C(GQK_Q3_K) C(GQK_Q4_K) C(GQK_Q5_K) C(GQK_Q6_K)

@@ -1128,8 +1128,12 @@ int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int type
   const uint16_t* xx = (const uint16_t*)x;
   uint16_t* yy = (uint16_t*)y;
   const uint16_t* bb = (const uint16_t*)bias;
+  if (bm == GQK_GEMV_SLAB && G == 8) {   // the mid form's slab: its x steps fit a static LDS block
+    if (nw != (nb + 1) / 2) return GQK_ERR_FORM;
+    return launch_gemv_mid(packed, desc, n_desc, types_mask, x, ldx, M, nw, true, y, ldy, bias, partials, counters, st);
+  }
   if (bm == GQK_GEMV_SLAB) {
-    // one wave per pair of super-blocks, the whole x in LDS
+    // one wave per pair of super-blocks, each staging its own x in LDS
     if (nw != (nb + 1) / 2 || nw > GQK_SLAB_MAX_WAVES || (G != 1 && G != 2) ||
         (G == 1 ? slab_lds_bytes<1>(nb, true) : slab_lds_bytes<2>(nb, true)) > GQK_SLAB_MAX_LDS)
       return GQK_ERR_FORM;
@@ -1139,7 +1143,7 @@ int launch_gemv(const uint8_t* packed, const int32_t* desc, int n_desc, int type
   }
   if (nw < 1 || nw > GQK_GEMV_MAX_WAVES) return GQK_ERR_FORM;
   const bool one = bm == 1;
-  if (G == 8) return launch_gemv_mid(packed, desc, n_desc, types_mask, x, ldx, M, nw, y, ldy, bias, partials, counters, st);
+  if (G == 8) return launch_gemv_mid(packed, desc, n_desc, types_mask, x, ldx, M, nw, false, y, ldy, bias, partials, counters, st);
   switch (G) {
 #define L(GG)                                                                                              \
     if (one) launch_g<GG, true>(types_mask, grid, nw, st, packed, desc, xx, ldx, M, yy, ldy, bb, part, counters); \

@@ -31,7 +31,7 @@ extern "C" {
 #define GQK_FORM_GEMV 1 /* M <= 32, every type: streaming forms over (tile, k-range) rows: the in-register
                            decode GEMV up to 16 rows (small shards up to 8 rows in its slab form,
                            plan bm = 2: a row per 32-row slab over the whole k-range), the mid form
-                           (g = 8) for 17..32 */
+                           (g = 8) for 17..32 (small shards at 9..32 rows in its slab form, bm = 2) */
 #define GQK_FORM_GEMM 2 /* M > 32: LDS-dequant bf16 MFMA GEMM (any M) */
 
 #define GQK_CTR_BYTES 262144 /* the arrival-counter region at the start of every workspace */
@@ -52,11 +52,13 @@ typedef struct gqk_shard {
 typedef struct gqk_plan_info {
   int32_t form;       /* GQK_FORM_GEMV or GQK_FORM_GEMM */
   int32_t m_max;      /* largest batch rows M the plan serves (GEMV: 4 * g) */
-  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4; 8 = the mid form, 17..32 rows) */
+  int32_t g;          /* GEMV: groups of 4 tokens (1, 2, 4; 8 = the mid form, 17..32 rows, or its slab
+                         form from 9 rows) */
   int32_t bm;         /* GEMM: tokens per tile (64, 128, 256); GEMV (g <= 2): 1 when every wave streams
                          exactly one 256-weight record (the launch takes the pipeline-free kernel),
                          2 for the slab form (a workgroup per 32-row half tile over the whole k-range,
-                         one wave per pair of super-blocks, no split-K partials) */
+                         one wave per pair of super-blocks, no split-K partials; with g = 8 the mid
+                         form's slab) */
   int32_t split;      /* GEMV: most workgroups sharing one tile (partials summed in split order in-kernel when > 1) */
   int32_t n_desc;     /* descriptor rows (workgroups along N x K) */
   int32_t types_mask; /* the GGML type of every shard, or 0 when the shards mix types */

@@ -136,7 +136,7 @@ def _check_slab_rows(shards, K, info, d):
     half), each over the whole k-range with no split (D_NC = 1), one wave per pair of super-blocks,
     no workspace.  Returns {tile: 1}."""
     nb = K // 256
-    assert info.split == 1 and info.workspace_bytes == 0 and info.nw == (nb + 1) // 2 and info.g <= 2
+    assert info.split == 1 and info.workspace_bytes == 0 and info.nw == (nb + 1) // 2 and info.g in (1, 2, 8)
     halves = {}
     col0 = 0
     cols = {}
@@ -156,20 +156,29 @@ def _check_slab_rows(shards, K, info, d):
 
 
 def test_plan_gemv_slab_form():
-    """The slab form (bm = 2) up to 8 rows: a workgroup per 32-row half tile over the whole
-    k-range when the slabs fill one round of the CUs, at least half of them, with K <= 6144 (one
-    wave per pair of super-blocks, each staging its own x in LDS)."""
+    """The slab form (bm = 2) up to 8 rows and at 17 to 32 (the mid form's slab): a workgroup per
+    32-row half tile over the whole k-range when the slabs fill one round of the CUs, at least half
+    of them, with K <= 6144 (one wave per pair of super-blocks); at 9 to 16 rows the mid form's
+    slab (g = 8) only when the slabs fill 7/8 of the CUs and no shard is IQ3_S."""
     from gguf_hip import ops
 
     qkv, o_proj = [(12, 7168, 0)], [(12, 5120, 0)]
-    for M in (1, 4, 5, 8):                                     # qkv: 224 slabs on 256 CUs
+    for M in (1, 4, 5, 8, 17, 32):                             # qkv: 224 slabs on 256 CUs
         info, desc = _plan(qkv, 5120, M)
         assert info.bm == 2 and info.n_desc == 224 and info.nw == 10, M
         _check_gemv_rows(qkv, 5120, info, desc)
-    for M in (1, 4, 5, 8):                                     # o_proj: 160 slabs
+    for M in (1, 4, 5, 8, 24):                                 # o_proj: 160 slabs
         assert _plan(o_proj, 5120, M)[0].bm == 2, M
     assert _plan([(12, 3968, 0)], 5120, 8)[0].bm != 2          # 124 slabs: under half the CUs
-    assert _plan(qkv, 5120, 9)[0].bm != 2                      # G = 4: not the slab form
+    assert _plan([(12, 3968, 0)], 5120, 32)[0].bm != 2
+    for M in (9, 16):                                          # 9..16 rows: 224 slabs >= 7/8 of 256
+        info, desc = _plan(qkv, 5120, M)
+        assert info.bm == 2 and info.g == 8 and info.m_max == 32, M
+        _check_gemv_rows(qkv, 5120, info, desc)
+        assert _plan(o_proj, 5120, M)[0].bm != 2               # 160 slabs: split-K
+        assert _plan([(21, 7168, 0)], 5120, M)[0].bm != 2      # IQ3_S: split-K
+        assert _plan([(21, 7168, 0)], 5120, M + 16)[0].bm == 2
+    assert _plan(qkv, 5120, 33)[0].form == 2                   # above 32 rows: the GEMM
     assert _plan([(12, 9216, 0)], 5120, 1)[0].bm != 2          # 288 slabs: more than one round
     assert _plan([(12, 2048, 0)], 5120, 1)[0].bm != 2          # 64 slabs: too few CUs busy
     assert _plan([(12, 7168, 0)], 25 * 256, 8)[0].bm != 2      # 25 super-blocks: above 12 waves

@@ -392,11 +392,13 @@ def _plan_of(gl, M):
 
 @pytest.mark.parametrize("wt", G.ALL_TYPES, ids=lambda t: G.NAMES[t])
 def test_gemv_slab_form(dev, wt):
-    """The slab form (up to 8 rows: a workgroup per 32-row half tile over the whole k-range, each
-    wave's x in LDS, the waves combined in LDS in a fixed order), planned on a pinned CU count so
-    that small shards take it: a last tile of <= 32 and of > 32 rows, an odd super-block count (a
-    half wave without a super-block), the largest k-range (24 super-blocks, 12 waves), a fused
-    bias, bit-identical repeats; against the oracle."""
+    """The slab form (a workgroup per 32-row half tile over the whole k-range, each wave's x in
+    LDS, the waves combined in LDS in a fixed order; up to 8 rows and, as the mid form's slab, 9
+    to 32 but for IQ3_S at 9 to 16), planned on a pinned CU count so that small shards take it: a
+    last tile of <= 32 and of
+    > 32 rows, an odd super-block count (a half wave without a super-block, or a wave of one
+    super-block), the largest k-range (24 super-blocks, 12 waves), a fused bias, bit-identical
+    repeats; against the oracle."""
     import gguf_hip
 
     rng = np.random.default_rng(900 + wt)
@@ -406,8 +408,8 @@ def test_gemv_slab_form(dev, wt):
         wf = G.dequantize(raw, wt)
         gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt], cus=cus)
         bias = (torch.randn(n, generator=torch.Generator().manual_seed(n)) * 4).to(torch.bfloat16).to(dev)
-        for M in (1, 3, 4, 5, 8):
-            assert _plan_of(gl, M).bm == 2, (n, nbk, M)
+        for M in (1, 3, 4, 5, 8, 12, 17, 24, 32):
+            assert (_plan_of(gl, M).bm == 2) == (wt != G.IQ3_S or not 9 <= M <= 16), (n, nbk, M)
             x = _x(M, K, 3000 + M, dev)
             y = gguf_hip.mul_mat_grouped(x, gl, bias)
             e = G.rel_err(y.float().cpu().numpy(), _ref(x, wf) + bias.float().cpu().numpy()[None])
@@ -432,7 +434,7 @@ def test_gemv_slab_form_mixed_layer(dev):
     gl = gguf_hip.pack_layer([torch.from_numpy(r).to(dev) for r in raws], [n for _, n in shards],
                              [wt for wt, _ in shards], cus=20)
     n_total = sum(n for _, n in shards)
-    for M in (2, 8):
+    for M in (2, 8, 20):
         info = _plan_of(gl, M)
         assert info.bm == 2 and info.types_mask == 0, M
         x = _x(M, K, 4000 + M, dev)
