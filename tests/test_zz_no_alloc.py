@@ -1,8 +1,9 @@
 """gqk_linear_noalloc (the entry point that allocates nothing: its workspace is a per-GPU device
 array) against gqk_linear with a caller workspace, through the C ABI: bit-identical outputs on
 two calls in a row, the second with fewer rows, for a split-K GEMV plan, a slab-form GEMV plan (no
-workspace at all), a stream-K GEMM plan and a mixed-type layer; a plan whose workspace exceeds the
-array is refused with an error."""
+workspace at all), the mid form (17..32 rows) in its slab and with its split-K exchange, a
+stream-K GEMM plan and a mixed-type layer; a plan whose workspace exceeds the array is refused
+with an error."""
 import ctypes
 
 import numpy as np
@@ -47,6 +48,8 @@ def test_noalloc_matches_linear_twice_then_smaller(dev):
     cases = [
         ("split-K GEMV", [(G.Q4_K, 900)], 4096, 0, (8, 3)),
         ("slab GEMV", [(G.Q6_K, 200)], 0, 8, (8, 3)),             # planned for 8 CUs: 7 slabs
+        ("mid slab", [(G.Q4_K, 200)], 0, 8, (30, 17)),            # the mid form's slab, 7 slabs
+        ("mid split-K", [(G.Q5_K, 900)], 4096, 0, (32, 20)),      # the mid form's exchange
         ("stream-K GEMM", [(G.Q6_K, 1000)], 0, 0, (60, 20)),
         ("mixed layer", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 2048, 0, (5, 2)),
         ("mixed layer GEMM", [(G.IQ4_XS, 130), (G.Q5_K, 300), (G.Q8_0, 64)], 0, 0, (100, 33)),
@@ -67,8 +70,10 @@ def test_noalloc_matches_linear_twice_then_smaller(dev):
             assert G.rel_err(y.float().cpu().numpy(), G.matmul_ref(x.float().cpu().numpy(), wf)) < 1e-2, (name, M)
         if name == "split-K GEMV":
             assert info.split > 1
-        if name == "slab GEMV":
+        if name in ("slab GEMV", "mid slab"):
             assert info.bm == 2 and info.workspace_bytes == 0
+        if name.startswith("mid"):
+            assert info.g == 8 and (info.split > 1) == (name == "mid split-K")
 
 
 def test_noalloc_refuses_a_plan_beyond_its_array(dev):
