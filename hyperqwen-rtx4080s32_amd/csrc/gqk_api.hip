@@ -295,21 +295,24 @@ int gqk_plan(const gqk_shard* shards, int nshards, int64_t K, int M, int target_
     // form's split-K exchange, whose 8 KiB of partials per workgroup cost ~30% of its launches
     // (eleven types at M = 17 / 32: qkv 5.6-9.8 us faster, o_proj 3.0-5.1; Q4_K qkv 20.7 -> 13.4 us
     // at 32).  At 9..16 rows it also beats the G = 4 GEMV when the slabs nearly fill the CUs (qkv,
-    // 224 of 256: 1.0-3.5 us faster at 12, except IQ3_S, 0.6-0.8 slower); at 160 slabs (o_proj) half the types are
-    // slower there, and up to 8 rows the GEMV slab is 1.5-4.8 us faster than it.  `down` (68
+    // 224 of 256: 1.0-3.5 us faster at 12, except IQ3_S, 0.6-0.8 slower); at 160 slabs (o_proj)
+    // only for the types of the lightest decode (M = 9 / 12 / 16: Q8_0 1.4-1.9 us, Q4_K 1.0-1.4,
+    // Q2_K 0.35-0.75, Q5_K 0.1-0.5 faster; Q3_K, Q6_K, IQ4_NL, IQ4_XS 0.3-1.3 and IQ3_S 2.5 slower).
+    // Up to 8 rows the GEMV slab is 1.5-4.8 us faster than it.  `down` (68
     // super-blocks, 12 waves of ~6) measured 3-7 us slower than split-K at 24-32 rows.
     int64_t slabs = 0;
-    bool any_iq = false, any_iq3s = false;
+    bool any_iq = false, any_iq3s = false, light = true;
     for (int i = 0; i < nshards; ++i) {
       const int64_t rem = shards[i].n % 64;
       slabs += 2 * ((shards[i].n + 63) / 64) - (rem != 0 && rem <= 32 ? 1 : 0);
       const int t = shards[i].ggml_type;
       any_iq |= t == GQK_IQ4_NL || t == GQK_IQ4_XS || t == GQK_IQ3_S;
       any_iq3s |= t == GQK_IQ3_S;
+      light &= t == GQK_Q8_0 || t == GQK_Q2_K || t == GQK_Q4_K || t == GQK_Q5_K;
     }
     const bool slab_fit =
         pi.g <= 2 ? nb * GQK_SLAB_SB_BYTES(pi.m_max) + (any_iq ? GQK_GEMV_TAB_BYTES : 0) <= GQK_SLAB_MAX_LDS
-                  : pi.g == 8 || (8 * slabs >= 7 * cus && !any_iq3s);
+                  : pi.g == 8 || (8 * slabs >= 7 * cus && !any_iq3s) || light;
     const bool slab = target_wgs <= 0 && nb <= 2 * GQK_SLAB_MAX_WAVES && slab_fit && 2 * slabs >= cus && slabs <= cus;
     if (slab) {
       if (pi.g == 4) {   // served by the mid form's slab (x padded to 32 tokens)

@@ -159,7 +159,8 @@ def test_plan_gemv_slab_form():
     """The slab form (bm = 2) up to 8 rows and at 17 to 32 (the mid form's slab): a workgroup per
     32-row half tile over the whole k-range when the slabs fill one round of the CUs, at least half
     of them, with K <= 6144 (one wave per pair of super-blocks); at 9 to 16 rows the mid form's
-    slab (g = 8) only when the slabs fill 7/8 of the CUs and no shard is IQ3_S."""
+    slab (g = 8) only when the slabs fill 7/8 of the CUs and no shard is IQ3_S, or every shard is
+    of a light-decode type (Q8_0, Q2_K, Q4_K, Q5_K)."""
     from gguf_hip import ops
 
     qkv, o_proj = [(12, 7168, 0)], [(12, 5120, 0)]
@@ -175,7 +176,8 @@ def test_plan_gemv_slab_form():
         info, desc = _plan(qkv, 5120, M)
         assert info.bm == 2 and info.g == 8 and info.m_max == 32, M
         _check_gemv_rows(qkv, 5120, info, desc)
-        assert _plan(o_proj, 5120, M)[0].bm != 2               # 160 slabs: split-K
+        assert _plan(o_proj, 5120, M)[0].bm == 2               # 160 slabs: Q4_K's light decode
+        assert _plan([(14, 5120, 0)], 5120, M)[0].bm != 2      # Q6_K there: split-K
         assert _plan([(21, 7168, 0)], 5120, M)[0].bm != 2      # IQ3_S: split-K
         assert _plan([(21, 7168, 0)], 5120, M + 16)[0].bm == 2
     assert _plan(qkv, 5120, 33)[0].form == 2                   # above 32 rows: the GEMM
