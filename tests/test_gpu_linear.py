@@ -421,6 +421,27 @@ def test_gemv_slab_form(dev, wt):
         assert G.rel_err(gguf_hip.mul_mat_grouped(x, gd).float().cpu().numpy(), _ref(x, wf)) < TOL
 
 
+def test_mid_slab_light_types_below_seven_eighths(dev):
+    """At 9..16 rows the mid form's slab also serves shards whose slabs fill less than 7/8 of the
+    CUs when every shard is of a light-decode type (Q4_K, Q5_K here: 7 slabs planned for 9 CUs),
+    and not a Q6_K shard of the same shape; both against the oracle."""
+    import gguf_hip
+
+    rng = np.random.default_rng(913)
+    n, K = 200, 5 * 256
+    for wt, slab in ((G.Q4_K, True), (G.Q5_K, True), (G.Q6_K, False)):
+        raw = G.random_blocks(rng, n, K, wt)
+        wf = G.dequantize(raw, wt)
+        gl = gguf_hip.pack_layer([torch.from_numpy(raw).to(dev)], [n], [wt], cus=9)
+        for M in (9, 12, 16):
+            info = _plan_of(gl, M)
+            assert (info.bm == 2 and info.g == 8) == slab, (G.NAMES[wt], M)
+            x = _x(M, K, 5000 + M, dev)
+            y = gguf_hip.mul_mat_grouped(x, gl)
+            e = G.rel_err(y.float().cpu().numpy(), _ref(x, wf))
+            assert e < TOL, (G.NAMES[wt], M, e)
+
+
 def test_gemv_slab_form_mixed_layer(dev):
     """A mixed-type layer (Q4_K, IQ4_XS with its LDS tables, Q6_K) in the slab form, written into a
     column slice of a wider output."""
