@@ -1042,7 +1042,8 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
   if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
-// The mid form's slab variant (17..32 rows, shards of at most one 32-row slab per CU): one
+// The mid form's slab variant (9..32 rows, x padded to 32 tokens; shards of at most one 32-row
+// slab per CU): one
 // workgroup per 32-row half (D_SPLIT) of a 64-row tile over the whole k-range, its waves splitting
 // the k-range as in the mid form (two super-blocks each at K = 5120) with one 32 x 32 block of
 // rows each; no split-K partials (whose 8 KiB per workgroup at 32 tokens made the exchange ~30% of
