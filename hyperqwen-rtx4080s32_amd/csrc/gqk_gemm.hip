@@ -915,7 +915,7 @@ __device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, cons
   }
 }
 
-#define MID_RED_BYTES (3 * 2 * 16 * 64 * 4)   // the waves' sums combined in LDS (nw <= 4)
+#define MID_RED_BYTES (3 * 2 * 16 * 64 * 4 + 16)   // the waves' sums combined in LDS (nw <= 4), a flag
 
 template <int ONLY>
 __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
@@ -970,76 +970,100 @@ __global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict
 
   // combine the waves (fixed order) in wave 0
   float* red = (float*)lds;   // [wave - 1][b][v][lane]
+  int* flag = (int*)(lds + 3 * 2 * 16 * 64 * 4);
   if (wave > 0)
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) red[(((wave - 1) * 2 + b) * 16 + v) * 64 + lane] = acc[b][v];
   __syncthreads();
-  if (wave > 0) return;
-  for (int w = 1; w < nw; ++w)
+  if (wave == 0)
+    for (int w = 1; w < nw; ++w)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[b][v] += red[(((w - 1) * 2 + b) * 16 + v) * 64 + lane];
+        for (int v = 0; v < 16; ++v) acc[b][v] += red[(((w - 1) * 2 + b) * 16 + v) * 64 + lane];
 
   // C block b: lane -> weight row 32 b + r, tokens 8 (v / 4) + 4 c + v % 4
   const int nvalid = dsc[D_NVALID];
   const int64_t col0 = dsc[D_COL0];
-  auto store_y = [&](int b, const v16f& a) {
-    const int row = 32 * b + r;
+  const int nc = dsc[D_NC];   // workgroups sharing this tile
+  // quarter qd of the outputs: block qd / 2, values 8 (qd % 2) .. + 7 of each lane
+  auto store_q = [&](int qd, const float (&a)[8]) {
+    const int b = qd >> 1, v0 = 8 * (qd & 1), row = 32 * b + r;
     if (row >= nvalid) return;
     // the layer bias (bf16 per output column) joins before the one rounding to bf16
     const float bv = bias != nullptr ? __builtin_bit_cast(float, (uint32_t)bias[col0 + row] << 16) : 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int t = 8 * (v >> 2) + 4 * c + (v & 3);
-      if (t < M) y[(int64_t)t * ldy + col0 + row] = __builtin_bit_cast(uint16_t, (__bf16)(a[v] + bv));
+    for (int e = 0; e < 8; ++e) {
+      const int v = v0 + e, t = 8 * (v >> 2) + 4 * c + (v & 3);
+      if (t < M) y[(int64_t)t * ldy + col0 + row] = __builtin_bit_cast(uint16_t, (__bf16)(a[e] + bv));
     }
   };
-  const int nc = dsc[D_NC];   // workgroups sharing this tile
   if (nc == 1) {
-    store_y(0, acc[0]);
-    store_y(1, acc[1]);
+    if (wave > 0) return;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = acc[qd >> 1][8 * (qd & 1) + e];
+      store_q(qd, a);
+    }
     return;
   }
   // Split-K exchange, as in the GEMV: the nc partials of a tile in slots D_SLOT0 .. + nc - 1 as
-  // [slot][64 rows][32 tokens], moved by device-coherent (sc1) 16-byte buffer accesses only; the
-  // stores complete before the arrival count, and the last workgroup to arrive sums the slots in
-  // split order, writes y and resets the counter for the next launch.
+  // [slot][64 rows][32 tokens], moved by device-coherent (sc1) 16-byte buffer accesses only.  Wave
+  // 0's sums go through LDS so that every wave stores quarters wave, wave + nw, .. of the partial;
+  // all stores complete before the arrival count (one barrier), and in the last workgroup to
+  // arrive every wave sums its quarters of the slots in split order and writes y; the counter is
+  // reset for the next launch.
+  __syncthreads();   // wave 0 has read the other waves' sums
+  if (wave == 0)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[(b * 16 + v) * 64 + lane] = acc[b][v];
+  __syncthreads();
   const int sp = dsc[D_SPLIT], ctr_i = dsc[D_CTR];
   float* tp = part + (int64_t)dsc[D_SLOT0] * 64 * MP;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(tp, 0, nc * 64 * MP * 4, GQK_GB_WORD3);
   auto soff = [&](int q, int b, int g) { return ((q * 64 + 32 * b + r) * MP + 8 * g + 4 * c) * 4; };
+  for (int qd = wave; qd < 4; qd += nw) {
+    const int b = qd >> 1, g0 = 2 * (qd & 1);
+    float a[8];
 #pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      __builtin_amdgcn_raw_buffer_store_b128(v4f{acc[b][4 * g], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]},
-                                             rs, soff(sp, b, g), 0, GQK_GB_SC1);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the partial stores are complete
-  int arrived = 0;
-  if (lane == 0) arrived = __hip_atomic_fetch_add(&ctr[ctr_i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  arrived = __shfl(arrived, 0);
-  if (arrived != nc - 1) return;
-  asm volatile("" ::: "memory");
-#pragma unroll
-  for (int b = 0; b < 2; ++b) {
-    v16f sum;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) sum[v] = 0.f;
-    for (int q = 0; q < nc; ++q) {
-      v4f t[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) t[g] = __builtin_amdgcn_raw_buffer_load_b128(rs, soff(q, b, g), 0, GQK_GB_SC1);
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum[4 * g + e] += t[g][e];
-    }
-    store_y(b, sum);
+    for (int e = 0; e < 8; ++e) a[e] = red[(b * 16 + 8 * (qd & 1) + e) * 64 + lane];
+    __builtin_amdgcn_raw_buffer_store_b128(v4f{a[0], a[1], a[2], a[3]}, rs, soff(sp, b, g0), 0, GQK_GB_SC1);
+    __builtin_amdgcn_raw_buffer_store_b128(v4f{a[4], a[5], a[6], a[7]}, rs, soff(sp, b, g0 + 1), 0, GQK_GB_SC1);
   }
-  if (lane == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's partial stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) *flag = __hip_atomic_fetch_add(&ctr[ctr_i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (*flag != nc - 1) return;
+  asm volatile("" ::: "memory");
+  constexpr int QB = 4;   // split slots per round trip (loads clamped to the last slot)
+  for (int qd = wave; qd < 4; qd += nw) {
+    const int b = qd >> 1, g0 = 2 * (qd & 1);
+    float a[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = 0.f;
+    for (int q0 = 0; q0 < nc; q0 += QB) {
+      v4f t[QB][2];
+#pragma unroll
+      for (int j = 0; j < QB; ++j)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+          t[j][h2] = __builtin_amdgcn_raw_buffer_load_b128(rs, soff(min(q0 + j, nc - 1), b, g0 + h2), 0, GQK_GB_SC1);
+#pragma unroll
+      for (int j = 0; j < QB; ++j)
+        if (q0 + j < nc)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[e] += t[j][e >> 2][e & 3];
+    }
+    store_q(qd, a);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&ctr[ctr_i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // next launch
 }
 
 // The mid form's slab variant (9..32 rows, x padded to 32 tokens; shards of at most one 32-row
