@@ -917,8 +917,11 @@ __device__ __forceinline__ void mid_wave(const uint8_t* __restrict__ tbase, cons
 
 #define MID_RED_BYTES (3 * 2 * 16 * 64 * 4 + 16)   // the waves' sums combined in LDS (nw <= 4), a flag
 
+// Three waves per SIMD for the two instances that would otherwise take just over 168 VGPRs (Q3_K
+// 170, the mixed-type build 176): Q3_K gate_up at M = 20 / 32 2.0-2.9 us faster; mixed layers
+// (gate_up, qkv + o_proj) 0.5-2.4 us faster even with the mixed build's 20 bytes of scratch.
 template <int ONLY>
-__global__ __launch_bounds__(256) void gemv_mid_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ONLY == GQK_Q3_K || ONLY == 0 ? 3 : 1))) void gemv_mid_kernel(const uint8_t* __restrict__ packed, const int32_t* __restrict__ desc,
                                                        const uint16_t* __restrict__ x, int64_t ldx, int M,
                                                        uint16_t* __restrict__ y, int64_t ldy,
                                                        const uint16_t* __restrict__ bias, float* __restrict__ part,
